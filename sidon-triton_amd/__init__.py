@@ -1,0 +1,29 @@
+"""sidon-triton_amd: the Sidon-Triton encoder's relative_key flash attention,
+rebuilt for MI355X (gfx950) as hand-written HIP behind a C ABI.
+
+Entry points (same argument meaning as the reference):
+  * ``flexrel.flexrel_attention(q, k, v, r, out=None, lens=None)`` --
+    src/sidon_triton/flexrel_triton.py:249 ([B, H, L, 64] strided views);
+  * ``encoder_attention.flexrel_attention(qkv, batch, heads, rel, lens)`` --
+    src/sidon_triton/triton_encoder.py:346 (fused QKV rows);
+  * ``graphs.BucketGraphs`` -- one HIP graph per length bucket
+    (src/sidon_triton/runtime.py:374-401).
+
+The package directory name is not a Python identifier; the repository's
+entry scripts load it under the module name ``sidon_triton_amd``.
+"""
+
+from . import _lib, encoder_attention, flexrel, graphs
+from .flexrel import HEAD_DIM, LEFT, NUM_POS, RIGHT, flexrel_attention
+
+__all__ = [
+    "HEAD_DIM",
+    "LEFT",
+    "NUM_POS",
+    "RIGHT",
+    "encoder_attention",
+    "flexrel",
+    "flexrel_attention",
+    "graphs",
+    "_lib",
+]

@@ -1,0 +1,179 @@
+"""GPU parity of the HIP kernel against the CPU oracle (needs an MI355X).
+
+Bar: on valid rows, output SNR >= 60 dB and
+max |err| <= 2e-3 against the float64 oracle on the same fp16 inputs; keys
+past the valid length contribute exactly zero (valid rows bit-identical when
+those keys hold finite garbage); every stored row finite.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import seeded_inputs
+from oracle.flexrel_oracle import errors, flexrel_reference
+
+pytestmark = pytest.mark.gpu
+
+SNR_DB = 60.0
+MAX_ABS = 2e-3
+DEV = torch.device("cuda:0")
+
+
+def run(sidon, q, k, v, rel, lens=None, out=None):
+    lens_t = None if lens is None else torch.tensor(lens, dtype=torch.int32, device=DEV)
+    res = sidon.flexrel.flexrel_attention(q.to(DEV), k.to(DEV), v.to(DEV), rel.to(DEV),
+                                          out=out, lens=lens_t)
+    torch.cuda.synchronize()
+    return res
+
+
+def assert_parity(ref, got, lens, label):
+    got = np.asarray(got, dtype=np.float64)
+    assert np.isfinite(got).all(), f"{label}: non-finite output"
+    for b, lk in enumerate(lens):
+        if lk == 0:
+            assert not got[b].any(), f"{label}: LK=0 rows must be zero"
+            continue
+        err = errors(ref[b, :, :lk], got[b, :, :lk])
+        print(f"{label} b={b} LK={lk}: snr={err['snr_db']:.1f} dB max_abs={err['max_abs']:.2e}",
+              flush=True)
+        assert err["snr_db"] >= SNR_DB and err["max_abs"] <= MAX_ABS, (label, b, err)
+
+
+CASES = [
+    # (B, H, L, lens)
+    (1, 1, 1, None),
+    (1, 2, 2, None),
+    (1, 2, 31, None),
+    (1, 2, 32, None),
+    (1, 2, 33, [20]),
+    (1, 2, 63, None),
+    (1, 2, 64, [64]),
+    (1, 2, 65, [65]),
+    (1, 2, 100, [1]),
+    (1, 3, 127, [127]),
+    (1, 2, 128, [100]),
+    (1, 2, 129, [129]),
+    (1, 2, 191, [190]),
+    (2, 2, 200, [200, 173]),
+    (1, 2, 257, [257]),
+    (3, 2, 300, [300, 64, 129]),
+    (1, 4, 513, [513]),
+    (2, 16, 100, [100, 77]),
+    (1, 16, 750, None),
+    (2, 1, 160, [0, 160]),
+]
+
+
+@pytest.mark.parametrize("B,H,L,lens", CASES)
+def test_parity_sweep(sidon, B, H, L, lens):
+    q, k, v, rel = seeded_inputs(B, H, L, seed=1000 + L + 7 * B)
+    got = run(sidon, q, k, v, rel, lens).float().cpu().numpy()
+    lens_list = [L] * B if lens is None else lens
+    ref = flexrel_reference(q.numpy(), k.numpy(), v.numpy(), rel.numpy(), lens_list)
+    assert_parity(ref, got, lens_list, f"B={B} H={H} L={L}")
+
+
+def test_golden_vectors(sidon, golden_cases):
+    """Against the transformers float64 outputs written by tests/golden/make_golden.py."""
+    for name, d in golden_cases.items():
+        q, k, v = (torch.from_numpy(d[x]) for x in ("q", "k", "v"))
+        rel = torch.from_numpy(d["rel"])
+        lens = [int(x) for x in d["lens"]]
+        got = run(sidon, q, k, v, rel, lens).float().cpu().numpy()
+        assert_parity(d["expected"], got, lens, name)
+
+
+def test_config1_fp32_inputs_L750(sidon):
+    """c1: fp32 q/k/v ~ N(0,1)/8, E ~ N(0, 0.02), cast to fp16; all rows vs the fp32-input oracle."""
+    q, k, v, rel = seeded_inputs(1, 16, 750, seed=1, dtype=np.float32, scale=0.125)
+    got = run(sidon, q.half(), k.half(), v.half(), rel.half()).float().cpu().numpy()
+    ref = flexrel_reference(q.numpy(), k.numpy(), v.numpy(), rel.numpy())
+    assert_parity(ref, got, [750], "c1")
+
+
+def test_config2_bucket_padding_L1500(sidon):
+    """c2: L=1500, LK=1463, padded K/V zero; then refilled with finite garbage -> bit-identical."""
+    L, LK = 1500, 1463
+    q, k, v, rel = seeded_inputs(1, 16, L, seed=2)
+    k[:, :, LK:] = 0
+    v[:, :, LK:] = 0
+    got = run(sidon, q, k, v, rel, [LK])
+    ref = flexrel_reference(q.numpy()[:, :, :LK], k.numpy()[:, :, :LK], v.numpy()[:, :, :LK], rel.numpy())
+    assert_parity(ref, got.float().cpu().numpy()[:, :, :LK], [LK], "c2")
+    gen = torch.Generator().manual_seed(22)
+    k2, v2, q2 = k.clone(), v.clone(), q.clone()
+    k2[:, :, LK:] = ((torch.rand(k2[:, :, LK:].shape, generator=gen) * 2 - 1) * 60000).half()
+    v2[:, :, LK:] = ((torch.rand(v2[:, :, LK:].shape, generator=gen) * 2 - 1) * 60000).half()
+    q2[:, :, LK:] = ((torch.rand(q2[:, :, LK:].shape, generator=gen) * 2 - 1) * 60000).half()
+    got2 = run(sidon, q2, k2, v2, rel, [LK])
+    assert torch.equal(got[:, :, :LK], got2[:, :, :LK]), "keys past LK changed valid rows"
+    assert torch.isfinite(got2.float()).all()
+
+
+def test_config3_one_layer_L4800(sidon):
+    """c3 shape (one layer, L=4800, H=16): 4 heads checked against the oracle, all finite."""
+    q, k, v, rel = seeded_inputs(1, 16, 4800, seed=3)
+    got = run(sidon, q, k, v, rel).float().cpu().numpy()
+    assert np.isfinite(got).all()
+    heads = [0, 5, 10, 15]
+    ref = flexrel_reference(q.numpy()[:, heads], k.numpy()[:, heads], v.numpy()[:, heads], rel.numpy())
+    assert_parity(ref, got[:, heads], [4800], "c3")
+
+
+def test_fused_qkv_layout_matches_strided(sidon):
+    """encoder layout (triton_encoder.py:346) == [B,H,L,64] views of the same buffer, bit for bit."""
+    B, H, L = 2, 16, 333
+    gen = torch.Generator().manual_seed(31)
+    qkv = torch.randn(B * L, 3 * H * 64, generator=gen).half().to(DEV)
+    rel = (torch.randn(73, 64, generator=gen) * 0.02).half().to(DEV)
+    lens = torch.tensor([333, 290], dtype=torch.int32, device=DEV)
+    ctx = sidon.encoder_attention.flexrel_attention(qkv, B, H, rel, lens)
+    view = qkv.view(B, L, 3, H, 64)
+    q, k, v = (view[:, :, i].permute(0, 2, 1, 3) for i in range(3))
+    out = sidon.flexrel.flexrel_attention(q, k, v, rel, lens=lens)
+    torch.cuda.synchronize()
+    assert torch.equal(ctx.view(B, L, H, 64).permute(0, 2, 1, 3), out)
+    ref = flexrel_reference(q.float().cpu().numpy(), k.float().cpu().numpy(), v.float().cpu().numpy(),
+                            rel.float().cpu().numpy(), [333, 290])
+    assert_parity(ref, out.float().cpu().numpy(), [333, 290], "qkv")
+
+
+def test_strided_output_view(sidon):
+    """out may be a strided view (row stride > 64); untouched memory stays untouched."""
+    B, H, L = 1, 2, 150
+    q, k, v, rel = seeded_inputs(B, H, L, seed=41)
+    big = torch.full((B, H, L, 128), 7.0, dtype=torch.float16, device=DEV)
+    out = big[..., 32:96]
+    run(sidon, q, k, v, rel, out=out)
+    assert torch.all(big[..., :32] == 7.0) and torch.all(big[..., 96:] == 7.0)
+    ref = flexrel_reference(q.numpy(), k.numpy(), v.numpy(), rel.numpy())
+    assert_parity(ref, out.float().cpu().numpy(), [L], "strided-out")
+
+
+def test_zero_table_matches_sdpa(sidon):
+    """E == 0 reduces to plain attention: compare with torch SDPA (fp32, CPU)."""
+    q, k, v, _ = seeded_inputs(1, 4, 400, seed=51)
+    rel = torch.zeros(73, 64, dtype=torch.float16)
+    got = run(sidon, q, k, v, rel).float().cpu()
+    ref = torch.nn.functional.scaled_dot_product_attention(q.float(), k.float(), v.float())
+    err = errors(ref.numpy(), got.numpy())
+    assert err["snr_db"] >= SNR_DB and err["max_abs"] <= MAX_ABS, err
+
+
+def test_deterministic(sidon):
+    q, k, v, rel = seeded_inputs(1, 16, 1000, seed=61)
+    a = run(sidon, q, k, v, rel, [917])
+    b = run(sidon, q, k, v, rel, [917])
+    assert torch.equal(a, b)
+
+
+def test_lens_clamped_to_length(sidon):
+    """lens > L reads nothing past the buffers (clamped to L)."""
+    q, k, v, rel = seeded_inputs(1, 2, 90, seed=71)
+    a = run(sidon, q, k, v, rel, [90])
+    b = run(sidon, q, k, v, rel, [100000])
+    assert torch.equal(a, b)
