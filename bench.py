@@ -2,9 +2,10 @@
 
 One step = one HIP-graph replay of the 8 attention calls of one 96 s chunk
 (B=1, H=16, L=4800, D=64, fp16 in/out, fp32 softmax), each layer with its own
-seeded 73x64 table.  Layer l+1's q/k/v come from layer l's output through a
-seeded projection (computed once, untimed; the inputs of every layer are
-resident in HBM before timing starts).  Prints ONE JSON line on stdout.
+seeded 73x64 table.  Layer l's q/k/v are the RMS-normalised residual stream
+times a seeded fused QKV projection, and layer l's output is added to the
+stream before layer l+1 (computed once, untimed: the inputs of every layer
+are resident in HBM before timing starts).  Prints ONE JSON line on stdout.
 
     python bench.py [--steps K] [--warmup W] [--no-cpu-baseline] [--no-check]
 
@@ -31,7 +32,8 @@ sys.path.insert(0, str(ROOT))
 METRIC = "ms per 96 s chunk (8-layer attn, L=4800); TFLOP/s and % fp16 MFMA peak"
 PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
 B, H, L, D, LAYERS = 1, 16, 4800, 64, 8
-TRAFFIC_FILE = ROOT / "profiles" / "flexrel_fwd_c3_traffic.json"
+TRAFFIC_FILE = ROOT / "profiles" / "flexrel_fwd_c3_traffic.md"
+COPY_PROBE_BYTES = 256 << 20  # --copy-probe: one device copy of this many bytes
 
 
 def log(*a):
@@ -43,20 +45,21 @@ def attention_flops(heads_total, lq, lk, dim=D):
 
 
 def build_inputs(torch, seed=0):
-    """Per-layer fused QKV [L, 3*H*64] fp16, tables [73, 64] fp16, projections [3072, 1024] fp16."""
+    """Residual stream h0 [L, 1024] fp32, per-layer tables [73, 64] fp16 and
+    fused QKV projections [3072, 1024] fp16 (seeded)."""
     gen = torch.Generator().manual_seed(seed)
     hid = H * D
-    qkv0 = torch.randn(B * L, 3 * hid, generator=gen).half()
+    h0 = torch.randn(B * L, hid, generator=gen)
     rels = [(torch.randn(73, D, generator=gen) * 0.02).half() for _ in range(LAYERS)]
     projs = [(torch.randn(3 * hid, hid, generator=gen) / math.sqrt(hid)).half() for _ in range(LAYERS)]
-    return qkv0, rels, projs
+    return h0, rels, projs
 
 
-def next_qkv(torch, ctx, proj):
-    """q/k/v source of the next layer: per-row RMS-normalised context times a seeded projection."""
-    x = ctx.float()
-    x = x * torch.rsqrt(x.square().mean(dim=1, keepdim=True) + 1e-6)
-    return x.half() @ proj.t()
+def qkv_of(torch, h, proj, out=None):
+    """q | k | v source of a layer: RMS-normalised residual stream times the
+    layer's projection (fp16 GEMM), [B*L, 3*H*64]; q/k/v come out ~N(0, 1)."""
+    x = h * torch.rsqrt(h.square().mean(dim=1, keepdim=True) + 1e-6)
+    return torch.matmul(x.half(), proj.t(), out=out)
 
 
 def cpu_baseline(torch, qkv0, rel0, heads):
@@ -94,6 +97,8 @@ def main() -> int:
     ap.add_argument("--cpu-heads", type=int, default=4)
     ap.add_argument("--no-check", action="store_true")
     ap.add_argument("--no-projections", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="only run 3 plain device copies of 256 MiB (calibrates the HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py runs on one GPU only: this build has no multi-GPU path "
@@ -101,6 +106,15 @@ def main() -> int:
         return 2
 
     import torch
+
+    if args.copy_probe:
+        src = torch.empty(COPY_PROBE_BYTES // 2, dtype=torch.float16, device="cuda:0").normal_()
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copy probe: 3 x {COPY_PROBE_BYTES} bytes read and written")
+        return 0
 
     from __graft_entry__ import load_package
 
@@ -110,18 +124,20 @@ def main() -> int:
     shape = sidon._lib.launch_shape(B, H, L)
     log(f"launch shape at L={L}: {shape}; {sidon._lib.version()}")
 
-    qkv0, rels, projs = build_inputs(torch)
+    h0, rels, projs = build_inputs(torch)
     rels_d = [r.to(dev) for r in rels]
     projs_d = [p.to(dev) for p in projs]
-    qkv = [qkv0.to(dev)]
     outs = [torch.empty(B * L, H * D, dtype=torch.float16, device=dev) for _ in range(LAYERS)]
     lens = torch.full((B,), L, dtype=torch.int32, device=dev)
     attn = sidon.encoder_attention.flexrel_attention
+    # Untimed: every layer's q/k/v, resident in HBM before timing starts.
     with torch.no_grad():
+        h = h0.to(dev)
+        qkv = []
         for i in range(LAYERS):
+            qkv.append(qkv_of(torch, h, projs_d[i]))
             attn(qkv[i], B, H, rels_d[i], lens, out=outs[i])
-            if i + 1 < LAYERS:
-                qkv.append(next_qkv(torch, outs[i], projs_d[i]))
+            h = h + outs[i].float()
     torch.cuda.synchronize()
 
     def enqueue_attention():
@@ -163,13 +179,18 @@ def main() -> int:
              "pct_fp16_peak": 100.0 * achieved / PEAK_TFLOPS, "launch": shape}
 
     if not args.no_projections:
+        # Secondary: the same 8 layers with the residual update and the next
+        # layer's projection between them (one graph).
+        h_d = h0.to(dev)
+        h_work = torch.empty_like(h_d)
+
         def enqueue_chain():
+            h_work.copy_(h_d)
             for i in range(LAYERS):
+                if i:
+                    qkv_of(torch, h_work, projs_d[i], out=qkv[i])
                 attn(qkv[i], B, H, rels_d[i], lens, out=outs[i])
-                if i + 1 < LAYERS:
-                    x = outs[i].float()
-                    x = x * torch.rsqrt(x.square().mean(dim=1, keepdim=True) + 1e-6)
-                    torch.matmul(x.half(), projs_d[i].t(), out=qkv[i + 1])
+                h_work.add_(outs[i])
         chain = graphs.capture(("chain", L), enqueue_chain)
         for _ in range(3):
             chain.replay()
@@ -186,17 +207,20 @@ def main() -> int:
     if not args.no_check:
         from oracle.flexrel_oracle import errors, flexrel_reference
         heads = [0, 15]
-        view = qkv[LAYERS - 1].view(B, L, 3, H, D).float().cpu().numpy()
-        q, k, v = (view[:, :, i, heads].transpose(0, 2, 1, 3) for i in range(3))
-        ref = flexrel_reference(q, k, v, rels[LAYERS - 1].float().numpy())
-        got = outs[LAYERS - 1].view(B, L, H, D)[:, :, heads].permute(0, 2, 1, 3).float().cpu().numpy()
-        err = errors(ref, got)
-        extra["check_last_layer_heads_0_15"] = err
-        log(f"parity (layer {LAYERS - 1}, heads {heads}): {err}")
+        for layer in (0, LAYERS - 1):
+            view = qkv[layer].view(B, L, 3, H, D).float().cpu().numpy()
+            q, k, v = (view[:, :, i, heads].transpose(0, 2, 1, 3) for i in range(3))
+            ref = flexrel_reference(q, k, v, rels[layer].float().numpy())
+            got = outs[layer].view(B, L, H, D)[:, :, heads].permute(0, 2, 1, 3).float().cpu().numpy()
+            err = errors(ref, got)
+            extra[f"check_layer{layer}_heads_0_15"] = err
+            log(f"parity (layer {layer}, heads {heads}): {err}")
 
     traffic = None
     if TRAFFIC_FILE.exists():
-        traffic = json.loads(TRAFFIC_FILE.read_text()).get("bytes_per_launch")
+        import re
+        m = re.search(r"HBM bytes per launch:\s*([0-9.eE+]+)", TRAFFIC_FILE.read_text())
+        traffic = float(m.group(1)) if m else None
 
     result = {
         "metric": METRIC,
@@ -210,7 +234,7 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp16",
-        "data": "synthetic (seeded q/k/v ~N(0,1), tables ~N(0,0.02), layer chain via seeded projections)",
+        "data": "synthetic (seeded residual stream ~N(0,1) -> RMS norm -> seeded fused QKV projection per layer, so q/k/v ~N(0,1); tables ~N(0,0.02))",
         "config": {"workload": "c3: 8 layers of relative_key attention, one 96 s chunk, graph replay",
                    "batch": B, "heads": H, "seq_len": L, "head_dim": D, "layers": LAYERS,
                    "valid_len": L, "parallelism": "none (1 GPU)"},
@@ -220,7 +244,7 @@ def main() -> int:
     result.update(extra)
     if not args.no_cpu_baseline:
         log("timing the CPU baseline ...")
-        result["cpu_baseline"] = cpu_baseline(torch, qkv0, rels[0], args.cpu_heads)
+        result["cpu_baseline"] = cpu_baseline(torch, qkv[0].cpu(), rels[0], args.cpu_heads)
     print(json.dumps(result), flush=True)
     return 0
 

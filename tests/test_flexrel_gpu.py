@@ -164,6 +164,26 @@ def test_zero_table_matches_sdpa(sidon):
     assert err["snr_db"] >= SNR_DB and err["max_abs"] <= MAX_ABS, err
 
 
+@pytest.mark.parametrize("direction", [1, -1])
+def test_growing_scores_force_max_updates(sidon, direction):
+    """Scores that grow along the keys by ~90 log2 units make the running max
+    stale many times over (probabilities would leave the fp16 range); the
+    exact max-update path must keep parity.  direction=-1 is the mirror."""
+    B, H, L = 1, 4, 1100
+    gen = torch.Generator().manual_seed(81)
+    q = torch.randn(B, H, L, 64, generator=gen) * 0.3 + 1.0
+    ramp = torch.linspace(0.0, 8.0, L)
+    if direction < 0:
+        ramp = ramp.flip(0)
+    k = (torch.randn(B, H, L, 64, generator=gen) * 0.3 + 1.0) * ramp[None, None, :, None]
+    v = torch.randn(B, H, L, 64, generator=gen)
+    rel = torch.randn(73, 64, generator=gen) * 0.5
+    q, k, v, rel = (t.half() for t in (q, k, v, rel))
+    got = run(sidon, q, k, v, rel, [1037]).float().cpu().numpy()
+    ref = flexrel_reference(q.numpy(), k.numpy(), v.numpy(), rel.numpy(), [1037])
+    assert_parity(ref, got, [1037], f"ramp{direction}")
+
+
 def test_deterministic(sidon):
     q, k, v, rel = seeded_inputs(1, 16, 1000, seed=61)
     a = run(sidon, q, k, v, rel, [917])
