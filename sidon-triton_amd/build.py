@@ -21,6 +21,8 @@ SOURCES = [PKG_DIR / "csrc" / "flexrel_fwd.hip"]
 ARCH = "gfx950"
 
 # -packed-fp32-ops: no v_pk_{add,mul,fma}_f32 in the generated code.
+# -amdgpu-mfma-vgpr-form: MFMA accumulators in ordinary VGPRs, so the softmax
+# reads the scores without AGPR copies (one wavefront per SIMD uses all 512).
 HIP_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",
@@ -30,6 +32,7 @@ HIP_FLAGS = [
     "-fvisibility=hidden",
     "-Wall",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 
 

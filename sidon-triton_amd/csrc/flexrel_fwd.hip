@@ -10,21 +10,18 @@
 // form of src/sidon_triton/flexrel_triton.py:249-278.
 //
 // Work decomposition.  One workgroup owns 64 query rows of one (b, h) and has
-// 8 wavefronts; wavefront w runs an independent online softmax over the w-th
-// eighth of the key range [0, LK) and the 8 partial results are merged
-// through LDS at the end.  Inside a wavefront the keys advance in steps of 32:
+// 8 wavefronts (two per SIMD); wavefront w runs an independent online softmax
+// over the key steps w, w + 8, w + 16, ... (32 keys each; round-robin, so the
+// few steps that need the per-score bias gather or the key mask fall at the
+// same time for all wavefronts) and the 8 partial results are merged through
+// LDS at the end.  Each wavefront runs a software pipeline in which every
+// dependency crosses a half-step boundary:
 //
-//   * wavefront w takes steps w, w + 8, w + 16, ... (round-robin, so the few
-//     steps that need the per-score bias gather or the key mask fall at the
-//     same time for all wavefronts of a workgroup);
 //   * K and V step tiles (32 keys x 64 dims, 4 KB each) are copied
 //     global -> LDS with global_load_lds_dwordx4 (no register staging) into a
-//     per-wavefront ring of two K and two V slots: the copy of K(u+2) and
-//     V(u+1) is in flight while step u computes.  16-byte chunks are XOR
-//     swizzled by row so both LDS read patterns below are bank-conflict free;
-//   * per step a wavefront runs an MFMA phase (S^T of step u, O^T update of
-//     step u - 1, then the copies and LDS operand reads for the next step)
-//     and a VALU-only softmax phase;
+//     per-wavefront ring of two K and two V slots; step u issues the copies
+//     of K(u+2) and V(u+1).  16-byte chunks are XOR swizzled by row so both
+//     LDS read patterns below are bank-conflict free;
 //   * scores are formed transposed, S^T = K . Q^T, with
 //     v_mfma_f32_32x32x16_f16 on two 32-query column blocks (Q^T stays in
 //     registers): every lane holds scores of one query only, so the softmax
@@ -34,13 +31,17 @@
 //     to fp16, is the B operand of O^T += V^T . P^T without any shuffle;
 //   * the V^T operand comes straight from the key-major V tile through
 //     ds_read_b64_tr_b16 (LDS transpose read);
+//   * step u is two scheduled half steps, one per column block: each issues
+//     4 QK and 4 PV MFMAs (of steps u and u - 1, or u - 1 and u + 1), one
+//     tile copy and the LDS operand reads of a later step among the exp2
+//     work of its column block;
 //   * softmax with a lazily updated running max: probabilities are
 //     exp2(s * log2(e)/8 + bias - m) with the max m of earlier steps.  While the
 //     step's probabilities stay inside the fp16 range (a lane's 16 values
 //     summing below 2^15), m, the row sum and O need no rescaling; a step
 //     that leaves it, and the first step, take the exact max-update path.
-//     The row sum is accumulated in fp32 with plain adds (v_dot2_f32_f16
-//     shares the matrix pipe and would stall the other wavefront's MFMAs);
+//     The row sum adds the fp16-rounded probabilities (v_fma_mix_f32), the
+//     same values the PV product uses;
 //   * relative bias: q . rel^T for the 64 rows x 73 positions is computed once
 //     per workgroup with MFMA into LDS (fp32).  Steps entirely left
 //     (j - i <= -64) or right (j - i >= 8) of a 32-row column block see a
@@ -56,6 +57,7 @@
 #include <string.h>
 
 #include <mutex>
+#include <type_traits>
 
 #include "sidon_flexrel.h"
 
@@ -69,19 +71,30 @@ constexpr int kRight = 8;
 constexpr int kNumPos = 73;     // rows of the relative table
 constexpr int kStep = 32;       // keys per pipeline step
 constexpr int kRows = 64;       // query rows per workgroup (two 32-column blocks)
-constexpr int kWaves = 8;       // key splits per workgroup, one wavefront each
+// Key splits per workgroup (wavefronts) and ring depth; 8 and 2 measured
+// fastest (4 x 3, one wavefront per SIMD, leaves the SIMDs idle on every
+// dependency stall).
+#ifndef SIDON_WAVES
+#define SIDON_WAVES 8
+#endif
+#ifndef SIDON_STAGES
+#define SIDON_STAGES 2
+#endif
+constexpr int kWaves = SIDON_WAVES;  // key splits per workgroup
 constexpr int kThreads = 64 * kWaves;
-constexpr int kTile = kStep * kD * 2;      // bytes of one K or V step tile
-constexpr int kWaveRing = 4 * kTile;       // K slot 0, K slot 1, V slot 0, V slot 1
-constexpr int kQrStride = 76;              // fp32 per row of the q.rel table
+constexpr int kStages = SIDON_STAGES;  // ring depth (K and V) per wavefront
+static_assert(kStages == 2 || kStages == 3, "ring depth");
+constexpr int kTile = kStep * kD * 2;        // bytes of one K or V step tile
+constexpr int kWaveRing = 2 * kStages * kTile;  // K slots, then V slots
+constexpr int kQrStride = 76;                // fp32 per row of the q.rel table
+constexpr int kQrOff = kWaves * kWaveRing;
+constexpr int kLdsBytes = kQrOff + kRows * kQrStride * 4;
 // A lane's 16 probabilities of one step summing below 2^15 are each below the
 // fp16 maximum, so their fp16 rounding is finite; a larger (or non-finite)
 // sum sends the query through the exact max update.
 constexpr float kSumLimit = 32768.f;
-constexpr int kQrOff = kWaves * kWaveRing;
-constexpr int kLdsBytes = kQrOff + kRows * kQrStride * 4;
 // Split merge (reuses the ring and table area after the key loop).
-constexpr int kMergeStride = 68;           // fp32 per partial-output row
+constexpr int kMergeStride = 68;             // fp32 per partial-output row
 constexpr int kMergeMlOff = kWaves * kRows * kMergeStride * 4;
 static_assert(kMergeMlOff + kWaves * kRows * 2 * 4 <= kLdsBytes, "merge area too small");
 static_assert(kLdsBytes <= 160 * 1024, "LDS budget of one CU");
@@ -143,23 +156,36 @@ __device__ __forceinline__ float pair_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// Asynchronous copy global -> LDS, 16 bytes per lane: lane l's bytes
-// gbase[voff_l .. +16) land at LDS byte address lds_addr + 16 l.  Issued as
-// inline assembly so that the compiler does not wait for the copy before
-// unrelated LDS reads; completion is awaited with wait_vmcnt below.
-// M0 is written here; nothing else in this translation unit uses M0 (the
-// clobber documents it -- the compiler treats M0 as reserved).
+// Asynchronous copy global -> LDS of one 4 KB tile: four instructions of
+// 64 lanes x 16 bytes.  Instruction i adds 1024 i to both addresses: lane l's
+// bytes gbase[voff_i,l + 1024 i .. +16) land at LDS byte address
+// lds_addr + 1024 i + 16 l.  Issued as inline assembly so that the compiler
+// does not wait for the copy before unrelated LDS reads; completion is
+// awaited with wait_vmcnt below.  M0 is written here; nothing else in this
+// translation unit uses M0 (the clobber documents it -- the compiler treats
+// M0 as reserved).
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void dma_x4(uint32_t lds_addr, const char* gbase, uint32_t voff) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
-               :: "s"(lds_addr), "v"(voff), "s"(gbase) : "memory", "m0");
+__device__ __forceinline__ void dma_tile(uint32_t lds_addr, const char* gbase, uint32_t v0, uint32_t v1,
+                                         uint32_t v2, uint32_t v3) {
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, %5\n\t"
+      "global_load_lds_dwordx4 %2, %5 offset:1024\n\t"
+      "global_load_lds_dwordx4 %3, %5 offset:2048\n\t"
+      "global_load_lds_dwordx4 %4, %5 offset:3072"
+      :: "s"(lds_addr), "v"(v0), "v"(v1), "v"(v2), "v"(v3), "s"(gbase) : "memory", "m0");
 }
 #pragma clang diagnostic pop
 
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory");
+}
+
+__device__ __forceinline__ void wait_lgkm0() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 }
 
 __device__ __forceinline__ void lds_barrier() {
@@ -208,62 +234,61 @@ flexrel_fwd_kernel(const Params p) {
   const int64_t kstride = (int64_t)p.ksl * 2;  // bytes
   const int64_t vstride = (int64_t)p.vsl * 2;
 
-  // Key steps: T steps of 32 keys cover [0, LK).  Wavefront w takes steps
-  // t = w + 8 u, u = 0 .. nu - 1 (round-robin, so the few "band" and masked
-  // steps of a workgroup fall into the same one or two phases).
+  // Key steps: T steps of 32 keys cover [0, LK); this wavefront takes steps
+  // w + 4 u, u = 0 .. nu - 1.
   const int T = (LK + kStep - 1) / kStep;
-  const int U = (T + kWaves - 1) / kWaves;          // phases of the slowest wavefront
   const int nu = T > w ? (T - w + kWaves - 1) / kWaves : 0;
   const bool active = nu > 0;
 
   char* ring = smem + w * kWaveRing;
   const uint32_t ring_lds = (uint32_t)(uintptr_t)LDS_PTR(char, ring);
 
-  // Copy of one step tile (K or V) into an LDS slot: 4 instructions of 64
-  // lanes x 16 bytes; LDS chunk position 64 i + lane = (row 8 i + lane / 8,
-  // swizzled chunk lane % 8).
+  // Copy of one step tile (K or V) into an LDS slot: LDS chunk position
+  // 64 i + lane = (row 8 i + lane / 8, swizzled chunk lane % 8).  Lane
+  // offsets are taken from base - 3072 (instruction i adds 1024 i), which
+  // keeps them non-negative.
   uint32_t koff[4], voff_own[4];
+  // Offsets for the last step T - 1 when it straddles LK: rows past LK re-read
+  // row LK - 1 (in bounds); their scores are masked.
+  uint32_t koff_last[4], voff_last_own[4];
+  const int last_row = LK - 1 - (T - 1) * kStep;  // in [0, 31]
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int r = 8 * i + (lane >> 3);
-    const uint32_t c16 = 16u * ((lane & 7) ^ tile_swz(r));
+    const int rc = min(r, last_row);
+    const uint32_t c16 = 16u * ((lane & 7) ^ tile_swz(r)) + 3072u - 1024u * i;
     koff[i] = (uint32_t)(r * kstride) + c16;
+    koff_last[i] = (uint32_t)(rc * kstride) + c16;
     voff_own[i] = kSameStride ? 0u : (uint32_t)(r * vstride) + c16;
+    voff_last_own[i] = kSameStride ? 0u : (uint32_t)(rc * vstride) + c16;
   }
   const uint32_t (&voff)[4] = kSameStride ? koff : voff_own;
-  // Local step u of this wavefront -> global step; local steps past the
-  // wavefront's range (prefetches whose data is never used) re-read step
-  // T - 1, so every copy stays in bounds and every phase issues the same
-  // number of copies.
+  const uint32_t (&voff_last)[4] = kSameStride ? koff_last : voff_last_own;
+  // Local step u -> global step; local steps past the wavefront's range
+  // (prefetches whose data is never used) re-read step T - 1, so every copy
+  // stays in bounds and every step issues the same number of copies.
   auto gstep = [&](int u) { return min(w + kWaves * u, T - 1); };
-  auto copy_tile = [&](const char* base, int64_t stride, const uint32_t (&off)[4], int u,
-                       uint32_t slot) {
-    const int k0 = gstep(u) * kStep;
-    const char* gb = base + (int64_t)k0 * stride;
-    if (k0 + kStep <= LK) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) dma_x4(slot + 1024u * i, gb, off[i]);
-    } else {
-      // Rows past LK re-read row LK - 1 (in bounds); their scores are masked.
-      const int last = LK - 1 - k0;  // >= 0: every step holds a valid key
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = 8 * i + (lane >> 3);
-        const uint32_t c16 = 16u * ((lane & 7) ^ tile_swz(r));
-        dma_x4(slot + 1024u * i, gb, (uint32_t)(min(r, last) * stride) + c16);
-      }
-    }
+  // may_straddle == false promises that step u is not T - 1 with LK % 32 != 0
+  // (no select then).  Branch-free, so a copy can sit in a scheduled block.
+  auto copy_tile = [&](const char* base, int64_t stride, const uint32_t (&off)[4],
+                       const uint32_t (&off_last)[4], int u, uint32_t slot, bool may_straddle) {
+    const int t = gstep(u);
+    const char* gb = base + (int64_t)(t * kStep) * stride - 3072;
+    const bool straddle = may_straddle && t == T - 1;
+    dma_tile(slot, gb, straddle ? off_last[0] : off[0], straddle ? off_last[1] : off[1],
+             straddle ? off_last[2] : off[2], straddle ? off_last[3] : off[3]);
   };
-  auto k_slot = [&](int u) { return ring_lds + (uint32_t)((u & 1) * kTile); };
-  auto v_slot = [&](int u) { return ring_lds + (uint32_t)(2 * kTile + (u & 1) * kTile); };
+  // Ring slots: K(u) and V(u) live in slot u % 3 of their halves of the ring.
+  constexpr uint32_t kVRing = kStages * kTile;
 
-  // First copies K(0), K(1), V(0) -- the steady-state order (K of the next
-  // step, then V of the current one) -- before the Q and table loads, so all
+  // First copies: K(0..2) and V(0..1) -- before the Q and table loads, so all
   // of them are in flight together.
   if (active) {
-    copy_tile(kbase, kstride, koff, 0, k_slot(0));
-    copy_tile(kbase, kstride, koff, 1, k_slot(1));
-    copy_tile(vbase, vstride, voff, 0, v_slot(0));
+#pragma unroll
+    for (int i = 0; i < kStages; ++i) copy_tile(kbase, kstride, koff, koff_last, i, ring_lds + i * kTile, true);
+#pragma unroll
+    for (int i = 0; i + 1 < kStages; ++i)
+      copy_tile(vbase, vstride, voff, voff_last, i, ring_lds + kVRing + i * kTile, true);
   }
 
   // Q^T as the MFMA B operand: lane (n, g) of block qb holds query
@@ -280,41 +305,34 @@ flexrel_fwd_kernel(const Params p) {
       for (int s = 0; s < 4; ++s) qop[qb][s] = h8{};
     }
   }
-  // rel rows for the q.rel table (wavefronts 0..5, see below); rows >= 73 are 0.
-  const int qr_pb = w % 3;
-  const int qr_qb = w / 3;
-  h8 eop[4];
-  {
-    const int pos = 32 * qr_pb + n;
-    const _Float16* src = p.rel + min(pos, kNumPos - 1) * kD + 8 * g;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) eop[s] = *reinterpret_cast<const h8*>(src + 16 * s);
-    if (pos >= kNumPos) {
-#pragma unroll
-      for (int s = 0; s < 4; ++s) eop[s] = h8{};
-    }
-  }
   // Every load above, the first tile copies included, has landed.  (A wait
   // the compiler sees, so it does not re-wait for these loads in the loop.)
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
 
-  // q.rel^T * scale for the 64 rows: wavefront w < 6 computes positions
-  // 32 (w % 3) + [0, 32) for column block w / 3 as rel . Q^T.
+  // q.rel^T * scale for the 64 rows: 6 blocks of 32 positions x 32 queries,
+  // block j = 3 qb + pb (positions 32 pb + [0, 32)) computed by wavefront
+  // j % 4 as rel . Q^T; rows of rel >= 73 are 0.
   float* qr_tab = reinterpret_cast<float*>(smem + kQrOff);
-  if (w < 6) {
+  for (int j = w; j < 6; j += kWaves) {
+    const int pb = j % 3;
+    const int qsel = j / 3;
+    const int pos = 32 * pb + n;
+    const _Float16* src = p.rel + min(pos, kNumPos - 1) * kD + 8 * g;
     f32x16 acc = {};
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      const h8 qsel = qr_qb ? qop[1][s] : qop[0][s];
-      acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(eop[s], qsel, acc, 0, 0, 0);
+      h8 e = *reinterpret_cast<const h8*>(src + 16 * s);
+      if (pos >= kNumPos) e = h8{};
+      const h8 qs = qsel ? qop[1][s] : qop[0][s];
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(e, qs, acc, 0, 0, 0);
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int pos0 = 32 * qr_pb + 8 * j + 4 * g;
+    for (int i = 0; i < 4; ++i) {
+      const int pos0 = 32 * pb + 8 * i + 4 * g;
       if (pos0 < kQrStride) {
-        const f4 val = {acc[4 * j] * scale, acc[4 * j + 1] * scale, acc[4 * j + 2] * scale,
-                        acc[4 * j + 3] * scale};
-        *reinterpret_cast<f4*>(qr_tab + (32 * qr_qb + n) * kQrStride + pos0) = val;
+        const f4 val = {acc[4 * i] * scale, acc[4 * i + 1] * scale, acc[4 * i + 2] * scale,
+                        acc[4 * i + 3] * scale};
+        *reinterpret_cast<f4*>(qr_tab + (32 * qsel + n) * kQrStride + pos0) = val;
       }
     }
   }
@@ -330,34 +348,31 @@ flexrel_fwd_kernel(const Params p) {
   f32x16 oacc[2][2] = {};   // O^T: dims 32 db + 8 (i/4) + 4 g + i%4, query n
   float m_run[2] = {-INFINITY, -INFINITY};
   float l_run[2] = {0.f, 0.f};
-  f32x16 sacc[2];           // S^T of the step in flight
-  h8 pk[2][2];              // fp16 probabilities: [column block][16-key half]
-  float lt[2];              // their sums
-  h8 kop[4] = {};           // K operands of the next QK product (k-steps 0..3)
-  h8 vop[2][2] = {};        // V^T operands of the next PV product [hh][db]
-  pk[0][0] = pk[0][1] = pk[1][0] = pk[1][1] = h8{};
+  float lt[2];              // probability sums of the current step
+  f32x16 sacc[2];           // S^T per column block (step u, or u + 1 once consumed)
+  h8 pk[2][2] = {};         // fp16 probabilities per column block and 16-key half
+  h8 kop[4];                // K operands (16 dims per k-step) of one step
+  h8 vop[2][2];             // V^T operands [hh][db] of one step
 
   // K operands: lane (m, g) holds key row perm(m) of the tile, dims
   // 16 s + 8 g + [0, 8).
   const int kperm = mfma_row_perm(n);
   const char* krow0 = ring + kperm * 128;
   const int kswz = tile_swz(kperm);
-  auto load_k = [&](int u) {
-    const char* krow = krow0 + (u & 1) * kTile;
+  auto load_k = [&](uint32_t slot) {
+    const char* krow = krow0 + slot;
 #pragma unroll
     for (int s = 0; s < 4; ++s)
       kop[s] = *reinterpret_cast<const h8*>(krow + (((2 * s + g) ^ kswz) << 4));
   };
   // V^T operands via transpose reads: group G of 16 lanes, source lane
   // (a, bq) reads V[key0 + a][d0 + 4 bq .. +4) with key0 = 16 hh + 8 (G / 2)
-  // + 4 hf and d0 = 32 db + 16 (G % 2).
+  // + 4 hf and d0 = 32 db + 16 (G % 2).  hh adds 2048 bytes (an immediate);
+  // hf and db flip one chunk bit each through the swizzle, so four per-lane
+  // bases cover all eight reads.
   const int tr_G = lane >> 4;
   const int tr_a = (lane >> 2) & 3;
   const int tr_b = lane & 3;
-  // Byte offset of the source of (hh, hf, db): row = 16 hh + 8 (G / 2) +
-  // 4 hf + a, chunk = (4 db + 2 (G % 2) + bq / 2) ^ tile_swz(row).  hh adds
-  // 2048 (an immediate); hf and db flip one chunk bit each through the
-  // swizzle, so four per-lane bases cover all eight reads.
   int tr_off[2][2];  // [hf][db] byte offset for hh = 0
 #pragma unroll
   for (int hf = 0; hf < 2; ++hf)
@@ -367,8 +382,8 @@ flexrel_fwd_kernel(const Params p) {
       const int chunk = 4 * db + 2 * (tr_G & 1) + (tr_b >> 1);
       tr_off[hf][db] = row * 128 + ((chunk ^ tile_swz(row)) << 4) + 8 * (tr_b & 1);
     }
-  auto load_v = [&](int u) {
-    const char* vt = ring + 2 * kTile + (u & 1) * kTile;
+  auto load_v = [&](uint32_t slot) {
+    const char* vt = ring + kVRing + slot;
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
 #pragma unroll
@@ -381,198 +396,220 @@ flexrel_fwd_kernel(const Params p) {
       }
     }
   };
-
-  // MFMA phase u: O^T += V^T(u - 1) . P^T(u - 1), then S^T(u) = K(u) . Q^T.
-  // Branch-free (one register assignment for O): where there is no step
-  // u - 1 the probabilities are 0 and add exactly 0 (V is finite), and past
-  // the wavefront's range S^T is computed on a valid dummy tile and unused.
-  // The K operands are read here (their latency hides behind the PV MFMAs);
-  // P is dead once PV is issued, so S^T can reuse its registers.
-  auto mfma_phase = [&](int u) {
-    load_k(u);
+  // S^T of column block qb = K . Q^T (4 MFMAs); O^T += V^T . P^T for column
+  // block qb (4 MFMAs).
+  auto qk = [&](int qb) {
+    sacc[qb] = f32x16{};
 #pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
+    for (int s = 0; s < 4; ++s)
+      sacc[qb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kop[s], qop[qb][s], sacc[qb], 0, 0, 0);
+  };
+  auto pv = [&](int qb) {
 #pragma unroll
-      for (int db = 0; db < 2; ++db) {
-        oacc[0][db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vop[hh][db], pk[0][hh], oacc[0][db], 0, 0, 0);
-        oacc[1][db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vop[hh][db], pk[1][hh], oacc[1][db], 0, 0, 0);
-      }
-    }
-    sacc[0] = f32x16{};
-    sacc[1] = f32x16{};
+    for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      sacc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kop[s], qop[0][s], sacc[0], 0, 0, 0);
-      sacc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kop[s], qop[1][s], sacc[1], 0, 0, 0);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    // While the MFMAs run: copies of K(u + 2) and V(u + 1) into the slots
-    // whose operands were read in phase u - 1; then K(u + 1) and V(u) (issued
-    // one phase earlier) have landed for the next two LDS operand reads.
-    if (u < nu) {
-      copy_tile(kbase, kstride, koff, u + 2, k_slot(u + 2));
-      copy_tile(vbase, vstride, voff, u + 1, v_slot(u + 1));
-      wait_vmcnt<8>();
-    }
+      for (int db = 0; db < 2; ++db)
+        oacc[qb][db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vop[hh][db], pk[qb][hh], oacc[qb][db], 0, 0, 0);
   };
 
-  // p = exp2(s * scale + nb) for a step without band or mask (nb = bias - m).
+  // The probability sums add the fp16-rounded values the PV product uses, so
+  // the normalisation matches the weights exactly (a dominant key keeps its
+  // V row unscaled).  fma(fp16 -> f32, one, sum) is a single v_fma_mix_f32;
+  // `one` is opaque so the multiply is not folded into a convert + add.
+  float one;
+  asm volatile("v_mov_b32 %0, 1.0" : "=v"(one));
+  // Round a pair of probabilities to fp16 (the PV operand) and add the
+  // rounded values to partial sum j % 4 (four independent chains; the same
+  // order on every path).
+  auto emit = [&](int qb, int i, const f2& e, float (&acc)[4]) {
+    const h2 ph = __builtin_convertvector(e, h2);
+    pk[qb][i >> 3][i & 7] = ph[0];
+    pk[qb][i >> 3][(i & 7) + 1] = ph[1];
+    float& a = acc[(i >> 1) & 3];
+    a = fmaf((float)ph[1], one, fmaf((float)ph[0], one, a));
+  };
+  auto finish = [&](int qb, const float (&acc)[4]) { lt[qb] = (acc[0] + acc[1]) + (acc[2] + acc[3]); };
+  // p = exp2(s * scale + nb) for column block qb (nb = bias - m).
   auto probs_fast = [&](int qb, float nb) {
-    float sum = 0.f;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const f2 e = {fast_exp2(fmaf(sacc[qb][8 * hh + 2 * j], scale, nb)),
-                      fast_exp2(fmaf(sacc[qb][8 * hh + 2 * j + 1], scale, nb))};
-        const h2 ph = __builtin_convertvector(e, h2);
-        pk[qb][hh][2 * j] = ph[0];
-        pk[qb][hh][2 * j + 1] = ph[1];
-        sum += e[0] + e[1];
-      }
-    }
-    lt[qb] = sum;
+    for (int i = 0; i < 16; i += 2)
+      emit(qb, i, f2{fast_exp2(fmaf(sacc[qb][i], scale, nb)), fast_exp2(fmaf(sacc[qb][i + 1], scale, nb))},
+           acc);
+    finish(qb, acc);
   };
   // p = exp2(y - m) from explicit biased scores y.
   auto probs_y = [&](int qb, const float (&y)[16], float m) {
-    float sum = 0.f;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const f2 e = {fast_exp2(y[8 * hh + 2 * j] - m), fast_exp2(y[8 * hh + 2 * j + 1] - m)};
-        const h2 ph = __builtin_convertvector(e, h2);
-        pk[qb][hh][2 * j] = ph[0];
-        pk[qb][hh][2 * j + 1] = ph[1];
-        sum += e[0] + e[1];
-      }
-    }
-    lt[qb] = sum;
+    for (int i = 0; i < 16; i += 2) emit(qb, i, f2{fast_exp2(y[i] - m), fast_exp2(y[i + 1] - m)}, acc);
+    finish(qb, acc);
   };
 
-  // Softmax phase u: probabilities of step u (from sacc), plus the copies and
-  // LDS operand reads that feed the next MFMA phase.
-  auto softmax_phase = [&](int u) {
-    if (u >= nu) {
-      // No step u: the next MFMA phase's PV adds nothing.
-      pk[0][0] = pk[0][1] = pk[1][0] = pk[1][1] = h8{};
-      return;
-    }
-
+  // Softmax of column block qb of step u, in its half step; then the exact
+  // max update where a query needs it (the first step, or a probability of
+  // this query left the fp16 range).  The decision is per query (lane
+  // pair), never per wavefront, so one row cannot change the rounding of
+  // another; and a row whose max does not change gets bit-identical values.
+  // Returns with the half step's MFMAs and LDS reads (issued by `work`)
+  // scheduled among the exp2 work of the fast case.
+  // A plain step (no band, no mask, not the first step) has the constant
+  // bias off_plain; the other steps redo the probabilities after the
+  // scheduled block.
+  auto half_step = [&](int u, int qb, auto&& dma, auto&& work, bool plain, float off_plain) {
     const int k0 = (w + kWaves * u) * kStep;
+    const int qlo = q0 + 32 * qb;
+    const bool left = k0 + (kStep - 1) - qlo <= -kLeft;
+    const bool right = k0 - (qlo + 31) >= kRight;
     const bool masked = k0 + kStep > LK;
-    bool band[2];
-    float off[2];
-#pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
-      const int qlo = q0 + 32 * qb;
-      const bool left = k0 + (kStep - 1) - qlo <= -kLeft;
-      const bool right = k0 - (qlo + 31) >= kRight;
-      band[qb] = !left && !right;
-      off[qb] = left ? qr_l[qb] : (right ? qr_r[qb] : 0.f);
-    }
+    const bool band = !left && !right;
     const bool first = u == 0;  // the running max is still -inf
+    const float off = left ? qr_l[qb] : (right ? qr_r[qb] : 0.f);
 
-    if (!first && !masked && !band[0] && !band[1]) {
-      probs_fast(0, off[0] - m_run[0]);
-      probs_fast(1, off[1] - m_run[1]);
-      if (__builtin_amdgcn_ballot_w64(!(fmaxf(lt[0], lt[1]) < kSumLimit)) != 0) {
-        // A probability of some query left the fp16 range: exact max update
-        // for those queries only (others keep bit-identical values).
+    // y = s * scale + bias (log2 units); masked keys -> -inf.
+    auto biased = [&](float (&y)[16]) {
+      if (band) {
+        const float* qrow = qr_tab + (32 * qb + n) * kQrStride;
+        const int d0 = k0 + 8 * g - (qlo + n) + kLeft;
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb) {
-          const bool need = pair_max(lt[qb] < kSumLimit ? 0.f : 1.f) > 0.f;
-          float mx = sacc[qb][0];
+        for (int i = 0; i < 16; ++i) {
+          const int idx = min(max(d0 + 16 * (i >> 3) + (i & 7), 0), kLeft + kRight);
+          y[i] = fmaf(sacc[qb][i], scale, qrow[idx]);
+        }
+      } else {
 #pragma unroll
-          for (int i = 1; i < 16; ++i) mx = fmaxf(mx, sacc[qb][i]);
-          mx = pair_max(fmaf(mx, scale, off[qb]));
-          const float m_new = need ? fmaxf(m_run[qb], mx) : m_run[qb];
-          const float alpha = fast_exp2(m_run[qb] - m_new);
-          l_run[qb] *= alpha;
-          oacc[qb][0] *= alpha;
-          oacc[qb][1] *= alpha;
-          m_run[qb] = m_new;
-          probs_fast(qb, off[qb] - m_new);
+        for (int i = 0; i < 16; ++i) y[i] = fmaf(sacc[qb][i], scale, off);
+      }
+      if (masked) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int key = k0 + 16 * (i >> 3) + 8 * g + (i & 7);
+          if (key >= LK) y[i] = -INFINITY;
         }
       }
-    } else {
-      // y = s * scale + bias (log2 units); masked keys -> -inf.
-      auto biased = [&](int qb, float (&y)[16]) {
-        if (band[qb]) {
-          const float* qrow = qr_tab + (32 * qb + n) * kQrStride;
-          const int d0 = k0 + 8 * g - (q0 + 32 * qb + n) + kLeft;
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int idx = min(max(d0 + 16 * (i >> 3) + (i & 7), 0), kLeft + kRight);
-            y[i] = fmaf(sacc[qb][i], scale, qrow[idx]);
-          }
-        } else {
-#pragma unroll
-          for (int i = 0; i < 16; ++i) y[i] = fmaf(sacc[qb][i], scale, off[qb]);
-        }
-        if (masked) {
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int key = k0 + 16 * (i >> 3) + 8 * g + (i & 7);
-            if (key >= LK) y[i] = -INFINITY;
-          }
-        }
-      };
-      // The same formula on the first call and after a max update, so rows
-      // whose max did not change get bit-identical values.
-      auto probs = [&](int qb, float m) {
-        if (band[qb] || masked) {
-          float y[16];
-          biased(qb, y);
-          probs_y(qb, y, m);
-        } else {
-          probs_fast(qb, off[qb] - m);
-        }
-      };
-      if (!first) {
-        probs(0, m_run[0]);
-        probs(1, m_run[1]);
+    };
+    auto probs = [&](float m) {
+      if (band || masked) {
+        float y[16];
+        biased(y);
+        probs_y(qb, y, m);
+      } else {
+        probs_fast(qb, off - m);
       }
-      if (first || __builtin_amdgcn_ballot_w64(!(fmaxf(lt[0], lt[1]) < kSumLimit)) != 0) {
-        // Exact max update for the queries that need it: the first step, or a
-        // probability of this query left the fp16 range.  The decision is per
-        // query (lane pair), never per wavefront, so one row cannot change
-        // the rounding of another.
+    };
+
+    // The LDS reads of the previous half step are done (so the slot refilled
+    // below is free), and the copy this half step reads, issued four half
+    // steps ago, has landed.
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0), seen by the compiler
+    wait_vmcnt<4 * (2 * kStages - 3)>();
+    // One basic block: the half step's MFMAs, LDS reads and tile copy among
+    // the exp2 work of the common case (no band, no mask, a running max).
+    // The other cases redo the probabilities below; the MFMAs never sit in a
+    // branch, so their accumulators stay in place.
+    __builtin_amdgcn_sched_barrier(0);
+    work();
+    dma();
+    probs_fast(qb, off_plain - m_run[qb]);
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb) {
-          const bool need = first || pair_max(lt[qb] < kSumLimit ? 0.f : 1.f) > 0.f;
-          float y[16];
-          biased(qb, y);
-          float mx = y[0];
-#pragma unroll
-          for (int i = 1; i < 16; ++i) mx = fmaxf(mx, y[i]);
-          mx = pair_max(mx);
-          const float m_new = need ? fmaxf(m_run[qb], mx) : m_run[qb];
-          const float alpha = fast_exp2(m_run[qb] - m_new);  // 1 if unchanged, 0 from -inf
-          l_run[qb] *= alpha;
-          oacc[qb][0] *= alpha;
-          oacc[qb][1] *= alpha;
-          m_run[qb] = m_new;
-          probs(qb, m_new);
-        }
-      }
+    for (int i = 0; i < 4; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+      __builtin_amdgcn_sched_group_barrier(0x402, 5, 0);  // 5 VALU
     }
-    l_run[0] += lt[0];
-    l_run[1] += lt[1];
-    load_v(u);  // V(u) operands for the next MFMA phase
+    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);    // DS reads
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+      __builtin_amdgcn_sched_group_barrier(0x402, 6, 0);  // 6 VALU
+    }
+    // Pin the common-case results here, so the compiler does not sink their
+    // computation into the branch below (out of the scheduled block).
+    asm volatile("" : "+v"(pk[qb][0]), "+v"(pk[qb][1]), "+v"(lt[qb]));
+    __builtin_amdgcn_sched_barrier(0);
+    if (!plain && !first) probs(m_run[qb]);
+    if (first || __builtin_amdgcn_ballot_w64(!(lt[qb] < kSumLimit)) != 0) {
+      const bool need = first || pair_max(lt[qb] < kSumLimit ? 0.f : 1.f) > 0.f;
+      float y[16];
+      biased(y);
+      float mx = y[0];
+#pragma unroll
+      for (int i = 1; i < 16; ++i) mx = fmaxf(mx, y[i]);
+      mx = pair_max(mx);
+      const float m_new = need ? fmaxf(m_run[qb], mx) : m_run[qb];
+      const float alpha = fast_exp2(m_run[qb] - m_new);  // 1 if unchanged, 0 from -inf
+      l_run[qb] *= alpha;
+      oacc[qb][0] *= alpha;
+      oacc[qb][1] *= alpha;
+      m_run[qb] = m_new;
+      probs(m_new);
+    }
+    l_run[qb] += lt[qb];
   };
 
-  // Each wavefront alternates an MFMA phase (PV of step u - 1, QK of step
-  // u, then the copies for later steps) and a softmax phase (VALU only, then
-  // the V operand reads of step u).  Wavefronts run free: the two sharing a SIMD drift
-  // apart, so one's matrix work tends to overlap the other's exp2 work.
-  for (int u = 0; u <= U; ++u) {
-    mfma_phase(u);
-    if (u < U) softmax_phase(u);
+  // Software pipeline over this wavefront's steps.  Step u is two half
+  // steps; every dependency crosses a half-step boundary and every register
+  // set is reused in place:
+  //   A(u): S^T(u) block 1 = K(u) . Q^T,  O^T block 0 += V^T(u-1) P^T(u-1),
+  //         read K(u+1) operands;         softmax of step u, block 0
+  //   B(u): O^T block 1 += V^T(u-1) P^T(u-1),  S^T(u+1) block 0 = K(u+1) . Q^T,
+  //         read V(u) operands;           softmax of step u, block 1
+  // With S = kStages ring slots per tensor, A(u) copies K(u+S) into the slot
+  // read during step u - 1 and B(u) copies V(u+S-1) into the slot V(u-1) was
+  // read from; the vmcnt before each half step leaves the 2S - 3 newest tile
+  // copies in flight, so K(u+1) has landed for A(u) and V(u) for B(u).
+  // c0, c1, c2 are the byte offsets of slots u % S, (u+1) % S, (u+2) % S.
+  if (active) {
+    load_k(0);
+    load_v(0);        // finite operands for the zero probabilities of step -1
+    qk(0);            // S^T(0) block 0
+    const bool ragged = LK % kStep != 0;  // step T - 1 straddles LK
+    uint32_t c0 = 0, c1 = kTile, c2 = 2 * kTile % (kStages * kTile);
+    for (int u = 0; u < nu; ++u) {
+      // Plain step: both column blocks entirely left (j - i <= -64) or both
+      // entirely right (j - i >= 8) of the window, and not the first or the
+      // masked step.
+      const int k0 = (w + kWaves * u) * kStep;
+      const bool both_left = k0 + (kStep - 1) - q0 <= -kLeft;
+      const bool both_right = k0 - (q0 + 63) >= kRight;
+      const bool plain = u > 0 && (both_left || both_right) && k0 + kStep <= LK;
+      const float off0 = both_left ? qr_l[0] : qr_r[0];
+      const float off1 = both_left ? qr_l[1] : qr_r[1];
+      half_step(
+          u, 0, [&]() { copy_tile(kbase, kstride, koff, koff_last, u + kStages, ring_lds + c0, ragged); },
+          [&]() {
+            qk(1);
+            pv(0);
+            load_k(c1);
+          },
+          plain, off0);
+      half_step(
+          u, 1,
+          [&]() {
+            copy_tile(vbase, vstride, voff, voff_last, u + kStages - 1,
+                      ring_lds + kVRing + (kStages == 3 ? c2 : c1), ragged);
+          },
+          [&]() {
+            pv(1);
+            qk(0);
+            load_v(c0);
+          },
+          plain, off1);
+      const uint32_t c = c0;
+      c0 = c1;
+      if (kStages == 3) {
+        c1 = c2;
+        c2 = c;
+      } else {
+        c1 = c;
+      }
+    }
+    wait_lgkm0();
+    pv(0);            // PV of the last step
+    pv(1);
   }
   wait_vmcnt<0>();  // the last (unused) prefetches have landed before LDS is reused
 
-  // ---- merge the 8 key splits ----
+  // ---- merge the key splits ----
   float l_tot[2];
 #pragma unroll
   for (int qb = 0; qb < 2; ++qb) l_tot[qb] = pair_sum(l_run[qb]);
@@ -599,31 +636,37 @@ flexrel_fwd_kernel(const Params p) {
   }
   lds_barrier();
 
-  // Wavefront w finalises rows 8 w + lane / 8, dims 8 (lane % 8) + [0, 8).
-  const int r = 8 * w + (lane >> 3);
-  const int c = 8 * (lane & 7);
+  // Wavefront w finalises kRows / kWaves rows, kCols dims per lane.
+  constexpr int kLanesPerRow = 64 / (kRows / kWaves);
+  constexpr int kCols = kD / kLanesPerRow;  // 16 (4 waves) or 8 (8 waves)
+  const int r = (kRows / kWaves) * w + lane / kLanesPerRow;
+  const int c = kCols * (lane % kLanesPerRow);
   float mmax = -INFINITY;
 #pragma unroll
   for (int s = 0; s < kWaves; ++s) mmax = fmaxf(mmax, ml[(s * kRows + r) * 2]);
   float lsum = 0.f;
-  f4 o0 = {0.f, 0.f, 0.f, 0.f};
-  f4 o1 = {0.f, 0.f, 0.f, 0.f};
+  f4 o[kCols / 4] = {};
 #pragma unroll
   for (int s = 0; s < kWaves; ++s) {
     const float ms = ml[(s * kRows + r) * 2];
     const float f = ms == -INFINITY ? 0.f : fast_exp2(ms - mmax);
     lsum += ml[(s * kRows + r) * 2 + 1] * f;
     const float* src = mo + (s * kRows + r) * kMergeStride + c;
-    o0 += *reinterpret_cast<const f4*>(src) * f;
-    o1 += *reinterpret_cast<const f4*>(src + 4) * f;
+#pragma unroll
+    for (int j = 0; j < kCols / 4; ++j) o[j] += *reinterpret_cast<const f4*>(src + 4 * j) * f;
   }
   const int row = q0 + r;
   if (row < p.L) {
     const float inv = lsum > 0.f ? __builtin_amdgcn_rcpf(lsum) : 0.f;
-    const h8 o = {(_Float16)(o0[0] * inv), (_Float16)(o0[1] * inv), (_Float16)(o0[2] * inv),
-                  (_Float16)(o0[3] * inv), (_Float16)(o1[0] * inv), (_Float16)(o1[1] * inv),
-                  (_Float16)(o1[2] * inv), (_Float16)(o1[3] * inv)};
-    *reinterpret_cast<h8*>(p.out + b * p.osb + h * p.osh + (int64_t)row * p.osl + c) = o;
+    _Float16* dst = p.out + b * p.osb + h * p.osh + (int64_t)row * p.osl + c;
+#pragma unroll
+    for (int j = 0; j < kCols / 8; ++j) {
+      const h8 v = {(_Float16)(o[2 * j][0] * inv), (_Float16)(o[2 * j][1] * inv),
+                    (_Float16)(o[2 * j][2] * inv), (_Float16)(o[2 * j][3] * inv),
+                    (_Float16)(o[2 * j + 1][0] * inv), (_Float16)(o[2 * j + 1][1] * inv),
+                    (_Float16)(o[2 * j + 1][2] * inv), (_Float16)(o[2 * j + 1][3] * inv)};
+      *reinterpret_cast<h8*>(dst + 8 * j) = v;
+    }
   }
 }
 
