@@ -62,6 +62,9 @@
 #include "sidon_flexrel.h"
 
 #define SIDON_API extern "C" __attribute__((visibility("default")))
+// Kernel-body lambdas index register arrays with their arguments; inlined,
+// every index is a constant and the arrays stay in registers.
+#define SIDON_INLINE __attribute__((always_inline))
 
 namespace {
 
@@ -71,24 +74,17 @@ constexpr int kRight = 8;
 constexpr int kNumPos = 73;     // rows of the relative table
 constexpr int kStep = 32;       // keys per pipeline step
 constexpr int kRows = 64;       // query rows per workgroup (two 32-column blocks)
-// Key splits per workgroup (wavefronts) and ring depth; 8 and 2 measured
-// fastest (4 x 3, one wavefront per SIMD, leaves the SIMDs idle on every
-// dependency stall).
-#ifndef SIDON_WAVES
-#define SIDON_WAVES 8
-#endif
-#ifndef SIDON_STAGES
-#define SIDON_STAGES 2
-#endif
-constexpr int kWaves = SIDON_WAVES;  // key splits per workgroup
+// Key splits per workgroup: 8 wavefronts, two per SIMD (one per SIMD leaves
+// the SIMD idle on every dependency stall of its wavefront).
+constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kStages = SIDON_STAGES;  // ring depth (K and V) per wavefront
-static_assert(kStages == 2 || kStages == 3, "ring depth");
+constexpr int kStages = 2;                   // ring depth (K and V) per wavefront
 constexpr int kTile = kStep * kD * 2;        // bytes of one K or V step tile
 constexpr int kWaveRing = 2 * kStages * kTile;  // K slots, then V slots
 constexpr int kQrStride = 76;                // fp32 per row of the q.rel table
 constexpr int kQrOff = kWaves * kWaveRing;
-constexpr int kLdsBytes = kQrOff + kRows * kQrStride * 4;
+constexpr int kQStageOff = kQrOff + kRows * kQrStride * 4;  // Q block, 64 rows x 128 B
+constexpr int kLdsBytes = kQStageOff + kRows * kD * 2;
 // A lane's 16 probabilities of one step summing below 2^15 are each below the
 // fp16 maximum, so their fp16 rounding is finite; a larger (or non-finite)
 // sum sends the query through the exact max update.
@@ -144,16 +140,12 @@ __device__ __forceinline__ int mfma_row_perm(int m) {
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // x of lane l and of lane l ^ 32 (the other half of the wavefront) combined
-// with max / sum.  v_permlane32_swap applied to (x, x) leaves one half's
+// with max.  v_permlane32_swap applied to (x, x) leaves one half's
 // value in each result register, so any symmetric combination of the two is
 // the combination over the lane pair.
 __device__ __forceinline__ float pair_max(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ __forceinline__ float pair_sum(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 // Asynchronous copy global -> LDS of one 4 KB tile: four instructions of
@@ -176,6 +168,10 @@ __device__ __forceinline__ void dma_tile(uint32_t lds_addr, const char* gbase, u
       "global_load_lds_dwordx4 %3, %5 offset:2048\n\t"
       "global_load_lds_dwordx4 %4, %5 offset:3072"
       :: "s"(lds_addr), "v"(v0), "v"(v1), "v"(v2), "v"(v3), "s"(gbase) : "memory", "m0");
+}
+__device__ __forceinline__ void dma_1k(uint32_t lds_addr, const char* gbase, uint32_t v0) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+               :: "s"(lds_addr), "v"(v0), "s"(gbase) : "memory", "m0");
 }
 #pragma clang diagnostic pop
 
@@ -267,7 +263,7 @@ flexrel_fwd_kernel(const Params p) {
   // Local step u -> global step; local steps past the wavefront's range
   // (prefetches whose data is never used) re-read step T - 1, so every copy
   // stays in bounds and every step issues the same number of copies.
-  auto gstep = [&](int u) { return min(w + kWaves * u, T - 1); };
+  auto gstep = [&](int u) SIDON_INLINE { return min(w + kWaves * u, T - 1); };
   // may_straddle == false promises that step u is not T - 1 with LK % 32 != 0
   // (no select then).  Branch-free, so a copy can sit in a scheduled block.
   auto copy_tile = [&](const char* base, int64_t stride, const uint32_t (&off)[4],
@@ -278,50 +274,77 @@ flexrel_fwd_kernel(const Params p) {
     dma_tile(slot, gb, straddle ? off_last[0] : off[0], straddle ? off_last[1] : off[1],
              straddle ? off_last[2] : off[2], straddle ? off_last[3] : off[3]);
   };
-  // Ring slots: K(u) and V(u) live in slot u % 3 of their halves of the ring.
+  // Ring slots: K(u) and V(u) live in slot u % kStages of their halves of the ring.
   constexpr uint32_t kVRing = kStages * kTile;
 
-  // First copies: K(0..2) and V(0..1) -- before the Q and table loads, so all
-  // of them are in flight together.
+  // First copies, all in flight together: this wavefront's 8 rows of the Q
+  // block into the Q staging area; the rel rows of its q.rel table block
+  // (wavefronts 0-5) into its last V slot, unused until step 0 refills it;
+  // and K(0), K(1), V(0).  Rows are clamped into range (Q rows >= L and rel
+  // rows >= 73 are zeroed after reading).  16-byte chunks are swizzled like
+  // the step tiles.
+  const uint32_t q_lds = (uint32_t)(uintptr_t)LDS_PTR(char, smem + kQStageOff);
+  {
+    const int r = 8 * w + (lane >> 3);
+    const int row0 = min(q0 + 8 * w, p.L - 1);
+    const char* gq = reinterpret_cast<const char*>(qbase + (int64_t)row0 * p.qsl);
+    const uint32_t off = (uint32_t)((min(q0 + r, p.L - 1) - row0) * p.qsl * 2) +
+                         16u * ((lane & 7) ^ tile_swz(r));
+    dma_1k(q_lds + 1024u * w, gq, off);
+  }
+  const int tab_j = w;  // q.rel block of this wavefront (if < 6): j = 3 qb + pb
+  if (tab_j < 6) {
+    const int pb = tab_j % 3;
+    uint32_t roff[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 8 * i + (lane >> 3);
+      roff[i] = (uint32_t)(min(32 * pb + r, kNumPos - 1) * kD * 2) + 16u * ((lane & 7) ^ tile_swz(r)) +
+                3072u - 1024u * i;
+    }
+    dma_tile(ring_lds + kVRing + (kStages - 1) * kTile, reinterpret_cast<const char*>(p.rel) - 3072,
+             roff[0], roff[1], roff[2], roff[3]);
+  }
   if (active) {
 #pragma unroll
     for (int i = 0; i < kStages; ++i) copy_tile(kbase, kstride, koff, koff_last, i, ring_lds + i * kTile, true);
 #pragma unroll
     for (int i = 0; i + 1 < kStages; ++i)
       copy_tile(vbase, vstride, voff, voff_last, i, ring_lds + kVRing + i * kTile, true);
+    wait_vmcnt<4 * (2 * kStages - 1)>();  // the Q rows and rel rows have landed
+  } else {
+    wait_vmcnt<0>();
   }
+  lds_barrier();  // the whole Q block is in LDS
 
   // Q^T as the MFMA B operand: lane (n, g) of block qb holds query
   // q0 + 32 qb + n, dims 16 s + 8 g + [0, 8) for k-step s.  Rows >= L are 0.
   h8 qop[2][4];
 #pragma unroll
   for (int qb = 0; qb < 2; ++qb) {
-    const int row = q0 + 32 * qb + n;
-    const _Float16* src = qbase + (int64_t)min(row, p.L - 1) * p.qsl + 8 * g;
+    const int r = 32 * qb + n;
+    const char* qrow = smem + kQStageOff + r * 128;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) qop[qb][s] = *reinterpret_cast<const h8*>(src + 16 * s);
-    if (row >= p.L) {
+    for (int s = 0; s < 4; ++s) qop[qb][s] = *reinterpret_cast<const h8*>(qrow + (((2 * s + g) ^ tile_swz(r)) << 4));
+    if (q0 + r >= p.L) {
 #pragma unroll
       for (int s = 0; s < 4; ++s) qop[qb][s] = h8{};
     }
   }
-  // Every load above, the first tile copies included, has landed.  (A wait
-  // the compiler sees, so it does not re-wait for these loads in the loop.)
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
 
   // q.rel^T * scale for the 64 rows: 6 blocks of 32 positions x 32 queries,
-  // block j = 3 qb + pb (positions 32 pb + [0, 32)) computed by wavefront
-  // j % 4 as rel . Q^T; rows of rel >= 73 are 0.
+  // block j = 3 qb + pb (positions 32 pb + [0, 32)) computed by wavefront j
+  // as rel . Q^T; rows of rel >= 73 are 0.
   float* qr_tab = reinterpret_cast<float*>(smem + kQrOff);
-  for (int j = w; j < 6; j += kWaves) {
-    const int pb = j % 3;
-    const int qsel = j / 3;
+  if (tab_j < 6) {
+    const int pb = tab_j % 3;
+    const int qsel = tab_j / 3;
     const int pos = 32 * pb + n;
-    const _Float16* src = p.rel + min(pos, kNumPos - 1) * kD + 8 * g;
+    const char* rrow = ring + kVRing + (kStages - 1) * kTile + n * 128;
     f32x16 acc = {};
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      h8 e = *reinterpret_cast<const h8*>(src + 16 * s);
+      h8 e = *reinterpret_cast<const h8*>(rrow + (((2 * s + g) ^ tile_swz(n)) << 4));
       if (pos >= kNumPos) e = h8{};
       const h8 qs = qsel ? qop[1][s] : qop[0][s];
       acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(e, qs, acc, 0, 0, 0);
@@ -347,8 +370,6 @@ flexrel_fwd_kernel(const Params p) {
 
   f32x16 oacc[2][2] = {};   // O^T: dims 32 db + 8 (i/4) + 4 g + i%4, query n
   float m_run[2] = {-INFINITY, -INFINITY};
-  float l_run[2] = {0.f, 0.f};
-  float lt[2];              // probability sums of the current step
   f32x16 sacc[2];           // S^T per column block (step u, or u + 1 once consumed)
   h8 pk[2][2] = {};         // fp16 probabilities per column block and 16-key half
   h8 kop[4];                // K operands (16 dims per k-step) of one step
@@ -359,7 +380,7 @@ flexrel_fwd_kernel(const Params p) {
   const int kperm = mfma_row_perm(n);
   const char* krow0 = ring + kperm * 128;
   const int kswz = tile_swz(kperm);
-  auto load_k = [&](uint32_t slot) {
+  auto load_k = [&](uint32_t slot) SIDON_INLINE {
     const char* krow = krow0 + slot;
 #pragma unroll
     for (int s = 0; s < 4; ++s)
@@ -382,7 +403,7 @@ flexrel_fwd_kernel(const Params p) {
       const int chunk = 4 * db + 2 * (tr_G & 1) + (tr_b >> 1);
       tr_off[hf][db] = row * 128 + ((chunk ^ tile_swz(row)) << 4) + 8 * (tr_b & 1);
     }
-  auto load_v = [&](uint32_t slot) {
+  auto load_v = [&](uint32_t slot) SIDON_INLINE {
     const char* vt = ring + kVRing + slot;
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
@@ -398,13 +419,13 @@ flexrel_fwd_kernel(const Params p) {
   };
   // S^T of column block qb = K . Q^T (4 MFMAs); O^T += V^T . P^T for column
   // block qb (4 MFMAs).
-  auto qk = [&](int qb) {
+  auto qk = [&](int qb) SIDON_INLINE {
     sacc[qb] = f32x16{};
 #pragma unroll
     for (int s = 0; s < 4; ++s)
       sacc[qb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kop[s], qop[qb][s], sacc[qb], 0, 0, 0);
   };
-  auto pv = [&](int qb) {
+  auto pv = [&](int qb) SIDON_INLINE {
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
@@ -412,60 +433,50 @@ flexrel_fwd_kernel(const Params p) {
         oacc[qb][db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vop[hh][db], pk[qb][hh], oacc[qb][db], 0, 0, 0);
   };
 
-  // The probability sums add the fp16-rounded values the PV product uses, so
-  // the normalisation matches the weights exactly (a dominant key keeps its
-  // V row unscaled).  fma(fp16 -> f32, one, sum) is a single v_fma_mix_f32;
-  // `one` is opaque so the multiply is not folded into a convert + add.
-  float one;
-  asm volatile("v_mov_b32 %0, 1.0" : "=v"(one));
-  // Round a pair of probabilities to fp16 (the PV operand) and add the
-  // rounded values to partial sum j % 4 (four independent chains; the same
-  // order on every path).
-  auto emit = [&](int qb, int i, const f2& e, float (&acc)[4]) {
+  // Row sums on the matrix core: rs = ones . P^T with v_mfma_f32_32x32x16_f16
+  // (the PV product's B operand layout), so every element of lane (n, g) is
+  // the step's sum of query n's fp16 probabilities -- the values the PV
+  // product uses.  Each output column reads its own query only, so a
+  // non-finite probability of one query never reaches another's sum.  One
+  // accumulator serves both column blocks: block 0's sums are read at the
+  // start of the half step that issues block 1's.
+  const h8 ones = {1, 1, 1, 1, 1, 1, 1, 1};
+  f32x16 rs;
+  float l_run[2] = {0.f, 0.f};
+  auto rowsum = [&](int qb) SIDON_INLINE {
+    rs = __builtin_amdgcn_mfma_f32_32x32x16_f16(ones, pk[qb][0], f32x16{}, 0, 0, 0);
+    rs = __builtin_amdgcn_mfma_f32_32x32x16_f16(ones, pk[qb][1], rs, 0, 0, 0);
+  };
+
+  // p = exp2(s * scale + nb) for column block qb (nb = bias - m), rounded to
+  // fp16: the B operand of the PV product.
+  auto emit = [&](int qb, int i, const f2& e) SIDON_INLINE {
     const h2 ph = __builtin_convertvector(e, h2);
     pk[qb][i >> 3][i & 7] = ph[0];
     pk[qb][i >> 3][(i & 7) + 1] = ph[1];
-    float& a = acc[(i >> 1) & 3];
-    a = fmaf((float)ph[1], one, fmaf((float)ph[0], one, a));
   };
-  auto finish = [&](int qb, const float (&acc)[4]) { lt[qb] = (acc[0] + acc[1]) + (acc[2] + acc[3]); };
-  // p = exp2(s * scale + nb) for column block qb (nb = bias - m).
-  auto probs_fast = [&](int qb, float nb) {
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  auto probs_fast = [&](int qb, float nb) SIDON_INLINE {
 #pragma unroll
     for (int i = 0; i < 16; i += 2)
-      emit(qb, i, f2{fast_exp2(fmaf(sacc[qb][i], scale, nb)), fast_exp2(fmaf(sacc[qb][i + 1], scale, nb))},
-           acc);
-    finish(qb, acc);
+      emit(qb, i, f2{fast_exp2(fmaf(sacc[qb][i], scale, nb)), fast_exp2(fmaf(sacc[qb][i + 1], scale, nb))});
   };
   // p = exp2(y - m) from explicit biased scores y.
   auto probs_y = [&](int qb, const float (&y)[16], float m) {
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < 16; i += 2) emit(qb, i, f2{fast_exp2(y[i] - m), fast_exp2(y[i + 1] - m)}, acc);
-    finish(qb, acc);
+    for (int i = 0; i < 16; i += 2) emit(qb, i, f2{fast_exp2(y[i] - m), fast_exp2(y[i + 1] - m)});
   };
 
-  // Softmax of column block qb of step u, in its half step; then the exact
-  // max update where a query needs it (the first step, or a probability of
-  // this query left the fp16 range).  The decision is per query (lane
-  // pair), never per wavefront, so one row cannot change the rounding of
-  // another; and a row whose max does not change gets bit-identical values.
-  // Returns with the half step's MFMAs and LDS reads (issued by `work`)
-  // scheduled among the exp2 work of the fast case.
-  // A plain step (no band, no mask, not the first step) has the constant
-  // bias off_plain; the other steps redo the probabilities after the
-  // scheduled block.
-  auto half_step = [&](int u, int qb, auto&& dma, auto&& work, bool plain, float off_plain) {
+  // Probabilities of column block qb of step u for the general cases (band
+  // gather, masked keys) and the exact max update, from the scores still in
+  // sacc[qb].
+  auto general = [&](int u, int qb, bool first, bool need_sum) SIDON_INLINE {
     const int k0 = (w + kWaves * u) * kStep;
     const int qlo = q0 + 32 * qb;
     const bool left = k0 + (kStep - 1) - qlo <= -kLeft;
     const bool right = k0 - (qlo + 31) >= kRight;
     const bool masked = k0 + kStep > LK;
     const bool band = !left && !right;
-    const bool first = u == 0;  // the running max is still -inf
     const float off = left ? qr_l[qb] : (right ? qr_r[qb] : 0.f);
-
     // y = s * scale + bias (log2 units); masked keys -> -inf.
     auto biased = [&](float (&y)[16]) {
       if (band) {
@@ -488,7 +499,7 @@ flexrel_fwd_kernel(const Params p) {
         }
       }
     };
-    auto probs = [&](float m) {
+    auto probs = [&](float m) SIDON_INLINE {
       if (band || masked) {
         float y[16];
         biased(y);
@@ -497,20 +508,64 @@ flexrel_fwd_kernel(const Params p) {
         probs_fast(qb, off - m);
       }
     };
+    // Recompute with the running max; then raise the max of the queries
+    // that need it: all at the first step (the max is -inf), else those whose
+    // step sum left the fp16-safe range (need_sum).  The decision is per
+    // query, never per wavefront, so one row cannot change the rounding of
+    // another; a row whose max does not change gets bit-identical values.
+    {
+      if (!first) probs(m_run[qb]);
+      if (first || need_sum) {
+        const bool need = first || !(rs[0] < kSumLimit);
+        float y[16];
+        biased(y);
+        float mx = y[0];
+#pragma unroll
+        for (int i = 1; i < 16; ++i) mx = fmaxf(mx, y[i]);
+        mx = pair_max(mx);
+        const float m_new = need ? fmaxf(m_run[qb], mx) : m_run[qb];
+        const float alpha = fast_exp2(m_run[qb] - m_new);  // 1 if unchanged, 0 from -inf
+        oacc[qb][0] *= alpha;
+        oacc[qb][1] *= alpha;
+        l_run[qb] *= alpha;
+        m_run[qb] = m_new;
+        probs(m_new);
+      }
+      rowsum(qb);
+    }
+  };
+  // Deferred check of block qb of step u (its row sums were issued a half
+  // step ago; its probabilities are consumed by the next PV product): a step
+  // sum outside the fp16-safe range sends the block through the max update.
+  // Then the step sums join the running sums.
+  auto settle = [&](int u, int qb) SIDON_INLINE {
+    if (__builtin_amdgcn_ballot_w64(!(rs[0] < kSumLimit)) != 0) general(u, qb, false, true);
+    l_run[qb] += rs[0];
+  };
 
+  // Softmax of column block qb of step u in its half step.  The half step's
+  // MFMAs, LDS reads and tile copy (issued by `work` and `dma`) are
+  // scheduled among the exp2 work of the common case: a plain step (no band,
+  // no mask, not the first step) with the constant bias off_plain.  The
+  // other steps redo the probabilities after the scheduled block.
+  auto half_step = [&](int u, int qb, auto&& dma, auto&& work, bool plain, float off_plain) SIDON_INLINE {
     // The LDS reads of the previous half step are done (so the slot refilled
-    // below is free), and the copy this half step reads, issued four half
-    // steps ago, has landed.
+    // below is free), and the copy this half step reads has landed.
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0), seen by the compiler
     wait_vmcnt<4 * (2 * kStages - 3)>();
-    // One basic block: the half step's MFMAs, LDS reads and tile copy among
-    // the exp2 work of the common case (no band, no mask, a running max).
-    // The other cases redo the probabilities below; the MFMAs never sit in a
-    // branch, so their accumulators stay in place.
+    // The other block's previous softmax, before its scores are overwritten.
+    if (qb == 0) {
+      if (u > 0) settle(u - 1, 1);
+    } else {
+      settle(u, 0);
+    }
+    // One basic block; the MFMAs never sit in a branch, so their
+    // accumulators stay in place.
     __builtin_amdgcn_sched_barrier(0);
     work();
     dma();
     probs_fast(qb, off_plain - m_run[qb]);
+    rowsum(qb);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
@@ -520,30 +575,14 @@ flexrel_fwd_kernel(const Params p) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
-      __builtin_amdgcn_sched_group_barrier(0x402, 6, 0);  // 6 VALU
+      __builtin_amdgcn_sched_group_barrier(0x402, 5, 0);  // 5 VALU
     }
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);    // row sums
     // Pin the common-case results here, so the compiler does not sink their
     // computation into the branch below (out of the scheduled block).
-    asm volatile("" : "+v"(pk[qb][0]), "+v"(pk[qb][1]), "+v"(lt[qb]));
+    asm volatile("" : "+v"(pk[qb][0]), "+v"(pk[qb][1]), "+v"(rs));
     __builtin_amdgcn_sched_barrier(0);
-    if (!plain && !first) probs(m_run[qb]);
-    if (first || __builtin_amdgcn_ballot_w64(!(lt[qb] < kSumLimit)) != 0) {
-      const bool need = first || pair_max(lt[qb] < kSumLimit ? 0.f : 1.f) > 0.f;
-      float y[16];
-      biased(y);
-      float mx = y[0];
-#pragma unroll
-      for (int i = 1; i < 16; ++i) mx = fmaxf(mx, y[i]);
-      mx = pair_max(mx);
-      const float m_new = need ? fmaxf(m_run[qb], mx) : m_run[qb];
-      const float alpha = fast_exp2(m_run[qb] - m_new);  // 1 if unchanged, 0 from -inf
-      l_run[qb] *= alpha;
-      oacc[qb][0] *= alpha;
-      oacc[qb][1] *= alpha;
-      m_run[qb] = m_new;
-      probs(m_new);
-    }
-    l_run[qb] += lt[qb];
+    if (!plain) general(u, qb, u == 0, false);
   };
 
   // Software pipeline over this wavefront's steps.  Step u is two half
@@ -559,12 +598,21 @@ flexrel_fwd_kernel(const Params p) {
   // copies in flight, so K(u+1) has landed for A(u) and V(u) for B(u).
   // c0, c1, c2 are the byte offsets of slots u % S, (u+1) % S, (u+2) % S.
   if (active) {
+    wait_vmcnt<0>();  // K(0), K(1), V(0)
     load_k(0);
     load_v(0);        // finite operands for the zero probabilities of step -1
     qk(0);            // S^T(0) block 0
     const bool ragged = LK % kStep != 0;  // step T - 1 straddles LK
     uint32_t c0 = 0, c1 = kTile, c2 = 2 * kTile % (kStages * kTile);
     for (int u = 0; u < nu; ++u) {
+      // Wavefronts w and w + 4 share a SIMD, and the issue arbiter favours
+      // the older one; alternate the wave priority per step so both finish
+      // together (a lone wavefront leaves its SIMD half idle).
+      if (((u + (w >> 2)) & 1) != 0) {
+        __builtin_amdgcn_s_setprio(1);
+      } else {
+        __builtin_amdgcn_s_setprio(0);
+      }
       // Plain step: both column blocks entirely left (j - i <= -64) or both
       // entirely right (j - i >= 8) of the window, and not the first or the
       // masked step.
@@ -603,6 +651,8 @@ flexrel_fwd_kernel(const Params p) {
         c1 = c;
       }
     }
+    __builtin_amdgcn_s_setprio(0);
+    settle(nu - 1, 1);
     wait_lgkm0();
     pv(0);            // PV of the last step
     pv(1);
@@ -612,7 +662,7 @@ flexrel_fwd_kernel(const Params p) {
   // ---- merge the key splits ----
   float l_tot[2];
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) l_tot[qb] = pair_sum(l_run[qb]);
+  for (int qb = 0; qb < 2; ++qb) l_tot[qb] = l_run[qb];
 
   lds_barrier();  // every wavefront is done with its ring and the q.rel table
   float* mo = reinterpret_cast<float*>(smem);
