@@ -31,17 +31,18 @@
 //     to fp16, is the B operand of O^T += V^T . P^T without any shuffle;
 //   * the V^T operand comes straight from the key-major V tile through
 //     ds_read_b64_tr_b16 (LDS transpose read);
-//   * step u is two scheduled half steps, one per column block: each issues
-//     4 QK and 4 PV MFMAs (of steps u and u - 1, or u - 1 and u + 1), one
-//     tile copy and the LDS operand reads of a later step among the exp2
-//     work of its column block;
+//   * step u is two half steps, one per column block: each issues 4 PV and
+//     4 QK MFMAs (of steps u - 1 and u, or u - 1 and u + 1), one tile copy
+//     and the LDS operand reads of a later step next to the exp2 work of
+//     its column block;
 //   * softmax with a lazily updated running max: probabilities are
 //     exp2(s * log2(e)/8 + bias - m) with the max m of earlier steps.  While the
-//     step's probabilities stay inside the fp16 range (a lane's 16 values
-//     summing below 2^15), m, the row sum and O need no rescaling; a step
-//     that leaves it, and the first step, take the exact max-update path.
-//     The row sum adds the fp16-rounded probabilities (v_fma_mix_f32), the
-//     same values the PV product uses;
+//     step's probabilities stay inside the fp16 range (a query's 32 values
+//     sum below 2^15), m, the row sum and O need no rescaling; a step that
+//     leaves it, and the first step, take the exact max-update path.  The
+//     row sums are taken on the matrix core from the fp16-rounded
+//     probabilities (the values the PV product uses) and checked one half
+//     step later, before the scores they came from are overwritten;
 //   * relative bias: q . rel^T for the 64 rows x 73 positions is computed once
 //     per workgroup with MFMA into LDS (fp32).  Steps entirely left
 //     (j - i <= -64) or right (j - i >= 8) of a 32-row column block see a
@@ -85,9 +86,9 @@ constexpr int kQrStride = 76;                // fp32 per row of the q.rel table
 constexpr int kQrOff = kWaves * kWaveRing;
 constexpr int kQStageOff = kQrOff + kRows * kQrStride * 4;  // Q block, 64 rows x 128 B
 constexpr int kLdsBytes = kQStageOff + kRows * kD * 2;
-// A lane's 16 probabilities of one step summing below 2^15 are each below the
-// fp16 maximum, so their fp16 rounding is finite; a larger (or non-finite)
-// sum sends the query through the exact max update.
+// A query's 32 probabilities of one step summing below 2^15 are each below
+// the fp16 maximum, so their fp16 rounding is finite; a larger (or
+// non-finite) sum sends the query through the exact max update.
 constexpr float kSumLimit = 32768.f;
 // Split merge (reuses the ring and table area after the key loop).
 constexpr int kMergeStride = 68;             // fp32 per partial-output row
@@ -122,12 +123,14 @@ struct Params {
   float scale;             // log2(e) / sqrt(64)
 };
 
-// 16-byte chunk c of tile row r is stored at chunk position c ^ tile_swz(r).
-// The map is a bijection of row bits 1..3, which keeps the 16 rows of every
-// ds_read_b128 quarter-wave on distinct banks, and puts row bit 1 on chunk
-// bit 1, which spreads the four rows of every ds_read_b64_tr_b16 group.
+// 16-byte chunk c of tile row r is stored at chunk position c ^ tile_swz(r)
+// (LDS: 64 banks of 4 bytes).  The map is a bijection of row bits 1..3, which
+// keeps the 16 rows of every 16-lane ds_read_b128 group on distinct banks.
+// It puts row bit 1 on chunk bit 2: a 32-lane half of a ds_read_b64_tr_b16
+// reads rows with bits 0-1 varying and chunk bits 0-1 varying (lane bits 1
+// and 4), so row bit 1 must land on the one chunk bit that does not vary.
 __device__ __forceinline__ int tile_swz(int row) {
-  return ((row >> 2) & 1) | (row & 2) | ((row >> 1) & 4);
+  return ((row >> 2) & 1) | ((row >> 2) & 2) | ((row << 1) & 4);
 }
 
 // Key row fed to A-operand lane m of S^T = K.Q^T: bits 2 and 3 of m swapped.
@@ -274,7 +277,13 @@ flexrel_fwd_kernel(const Params p) {
     dma_tile(slot, gb, straddle ? off_last[0] : off[0], straddle ? off_last[1] : off[1],
              straddle ? off_last[2] : off[2], straddle ? off_last[3] : off[3]);
   };
-  // Ring slots: K(u) and V(u) live in slot u % kStages of their halves of the ring.
+  // Copy of a tile from gb (its first row, minus 3072) into an LDS slot.
+  auto copy_from = [&](const char* gb, const uint32_t (&off)[4], const uint32_t (&off_last)[4], uint32_t slot,
+                       bool straddle) SIDON_INLINE {
+    dma_tile(slot, gb, straddle ? off_last[0] : off[0], straddle ? off_last[1] : off[1],
+             straddle ? off_last[2] : off[2], straddle ? off_last[3] : off[3]);
+  };
+  // Ring slots: K(u) and V(u) live in slot u % 2 of their halves of the ring.
   constexpr uint32_t kVRing = kStages * kTile;
 
   // First copies, all in flight together: this wavefront's 8 rows of the Q
@@ -455,10 +464,12 @@ flexrel_fwd_kernel(const Params p) {
     pk[qb][i >> 3][i & 7] = ph[0];
     pk[qb][i >> 3][(i & 7) + 1] = ph[1];
   };
-  auto probs_fast = [&](int qb, float nb) SIDON_INLINE {
+  // Keys [8 part, 8 part + 8) of the lane's 16 (part -1: all).
+  auto probs_fast = [&](int qb, float nb, int part = -1) SIDON_INLINE {
 #pragma unroll
     for (int i = 0; i < 16; i += 2)
-      emit(qb, i, f2{fast_exp2(fmaf(sacc[qb][i], scale, nb)), fast_exp2(fmaf(sacc[qb][i + 1], scale, nb))});
+      if (part < 0 || (i >> 3) == part)
+        emit(qb, i, f2{fast_exp2(fmaf(sacc[qb][i], scale, nb)), fast_exp2(fmaf(sacc[qb][i + 1], scale, nb))});
   };
   // p = exp2(y - m) from explicit biased scores y.
   auto probs_y = [&](int qb, const float (&y)[16], float m) {
@@ -539,71 +550,88 @@ flexrel_fwd_kernel(const Params p) {
   // sum outside the fp16-safe range sends the block through the max update.
   // Then the step sums join the running sums.
   auto settle = [&](int u, int qb) SIDON_INLINE {
-    if (__builtin_amdgcn_ballot_w64(!(rs[0] < kSumLimit)) != 0) general(u, qb, false, true);
+    // All of rs stays live up to here, so no register of the in-flight row
+    // sum is reused (and waited for) before it lands.
+    asm volatile("" : "+v"(rs));
+    if (__builtin_expect(__builtin_amdgcn_ballot_w64(!(rs[0] < kSumLimit)) != 0, 0)) general(u, qb, false, true);
     l_run[qb] += rs[0];
   };
 
-  // Softmax of column block qb of step u in its half step.  The half step's
-  // MFMAs, LDS reads and tile copy (issued by `work` and `dma`) are
-  // scheduled among the exp2 work of the common case: a plain step (no band,
-  // no mask, not the first step) with the constant bias off_plain.  The
-  // other steps redo the probabilities after the scheduled block.
-  auto half_step = [&](int u, int qb, auto&& dma, auto&& work, bool plain, float off_plain) SIDON_INLINE {
+  // Softmax of column block qb of step u in its half step, in two parts
+  // around the settling of the other block's previous softmax:
+  //   1. `pre` (the PV product, 4 MFMAs) and the exp2 work of keys 0-7;
+  //   2. `post` (the QK product, 4 MFMAs, and the next operand reads), the
+  //      tile copy `dma`, keys 8-15 and the row sums (2 MFMAs).
+  // The settle sits between them: the row sums it reads have had the PV
+  // product's time to land, and `post` overwrites the scores it may need.
+  // The common case is a plain step (no band, no mask, not the first step)
+  // with the constant bias off_plain; the other steps redo the
+  // probabilities at the end.  The MFMAs never sit in a branch, so their
+  // accumulators stay in place.  (Instruction order inside each part is left
+  // to the compiler: with two wavefronts per SIMD it interleaves MFMA and
+  // VALU work across them better than a fixed in-wave pattern.)
+  auto half_step = [&](int u, int qb, auto&& dma, auto&& pre, auto&& post, bool plain,
+                       float off_plain) SIDON_INLINE {
     // The LDS reads of the previous half step are done (so the slot refilled
     // below is free), and the copy this half step reads has landed.
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0), seen by the compiler
     wait_vmcnt<4 * (2 * kStages - 3)>();
-    // The other block's previous softmax, before its scores are overwritten.
+    const float nb = off_plain - m_run[qb];
+    pre();
+    probs_fast(qb, nb, 0);
+    asm volatile("" : "+v"(pk[qb][0]));
     if (qb == 0) {
       if (u > 0) settle(u - 1, 1);
     } else {
       settle(u, 0);
     }
-    // One basic block; the MFMAs never sit in a branch, so their
-    // accumulators stay in place.
-    __builtin_amdgcn_sched_barrier(0);
-    work();
+    post();
     dma();
-    probs_fast(qb, off_plain - m_run[qb]);
+    probs_fast(qb, nb, 1);
     rowsum(qb);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
-      __builtin_amdgcn_sched_group_barrier(0x402, 5, 0);  // 5 VALU
-    }
-    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);    // DS reads
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
-      __builtin_amdgcn_sched_group_barrier(0x402, 5, 0);  // 5 VALU
-    }
-    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);    // row sums
     // Pin the common-case results here, so the compiler does not sink their
-    // computation into the branch below (out of the scheduled block).
-    asm volatile("" : "+v"(pk[qb][0]), "+v"(pk[qb][1]), "+v"(rs));
-    __builtin_amdgcn_sched_barrier(0);
-    if (!plain) general(u, qb, u == 0, false);
+    // computation into the branch below.
+    asm volatile("" : "+v"(pk[qb][0]), "+v"(pk[qb][1]));
+    if (__builtin_expect(!plain, 0)) general(u, qb, u == 0, false);
   };
 
   // Software pipeline over this wavefront's steps.  Step u is two half
   // steps; every dependency crosses a half-step boundary and every register
   // set is reused in place:
-  //   A(u): S^T(u) block 1 = K(u) . Q^T,  O^T block 0 += V^T(u-1) P^T(u-1),
-  //         read K(u+1) operands;         softmax of step u, block 0
-  //   B(u): O^T block 1 += V^T(u-1) P^T(u-1),  S^T(u+1) block 0 = K(u+1) . Q^T,
-  //         read V(u) operands;           softmax of step u, block 1
-  // With S = kStages ring slots per tensor, A(u) copies K(u+S) into the slot
-  // read during step u - 1 and B(u) copies V(u+S-1) into the slot V(u-1) was
-  // read from; the vmcnt before each half step leaves the 2S - 3 newest tile
-  // copies in flight, so K(u+1) has landed for A(u) and V(u) for B(u).
-  // c0, c1, c2 are the byte offsets of slots u % S, (u+1) % S, (u+2) % S.
+  //   A(u): O^T block 0 += V^T(u-1) P^T(u-1);  settle block 1 of step u-1;
+  //         S^T(u) block 1 = K(u) . Q^T, read K(u+1) operands;
+  //         softmax of step u, block 0
+  //   B(u): O^T block 1 += V^T(u-1) P^T(u-1);  settle block 0 of step u;
+  //         S^T(u+1) block 0 = K(u+1) . Q^T, read V(u) operands;
+  //         softmax of step u, block 1
+  // The ring has two K and two V slots: A(u) copies K(u+2) into the slot
+  // K(u) was read from (during A(u-1)), B(u) copies V(u+1) into the slot V(u-1)
+  // was read from; the vmcnt(4) before each half step leaves only the newest
+  // copy in flight, so K(u+1) has landed for A(u) and V(u) for B(u).  c0 and
+  // c1 are the byte offsets of slots u % 2 and (u+1) % 2.
   if (active) {
     wait_vmcnt<0>();  // K(0), K(1), V(0)
     load_k(0);
     load_v(0);        // finite operands for the zero probabilities of step -1
     qk(0);            // S^T(0) block 0
     const bool ragged = LK % kStep != 0;  // step T - 1 straddles LK
-    uint32_t c0 = 0, c1 = kTile, c2 = 2 * kTile % (kStages * kTile);
+    // Plain steps (see half_step) are u in [1, uM) with u <= uL (both column
+    // blocks entirely left of the window, j - i <= -64) or u >= uR (both
+    // entirely right, j - i >= 8); uM is the first step that straddles LK.
+    // (Arithmetic shifts: floor and ceiling divisions by 256 = 8 steps of 32.)
+    const int uL = (q0 - 95 - kStep * w) >> 8;
+    const int uR = -((-(q0 + 71 - kStep * w)) >> 8);
+    const int uM = ((LK - kStep - kStep * w) >> 8) + 1;
+    // Tile sources, advanced by 8 steps per step of this wavefront; copies
+    // of step T - 1 (the last one, also for prefetches past the range) read
+    // from klast / vlast with the straddle offsets.
+    const int64_t kinc = (int64_t)kWaves * kStep * kstride;
+    const int64_t vinc = (int64_t)kWaves * kStep * vstride;
+    const char* gk = kbase + (int64_t)(w + 2 * kWaves) * kStep * kstride - 3072;  // K(2)
+    const char* gv = vbase + (int64_t)(w + kWaves) * kStep * vstride - 3072;      // V(1)
+    const char* klast = kbase + (int64_t)(T - 1) * kStep * kstride - 3072;
+    const char* vlast = vbase + (int64_t)(T - 1) * kStep * vstride - 3072;
+    uint32_t c0 = 0, c1 = kTile;
     for (int u = 0; u < nu; ++u) {
       // Wavefronts w and w + 4 share a SIMD, and the issue arbiter favours
       // the older one; alternate the wave priority per step so both finish
@@ -616,40 +644,39 @@ flexrel_fwd_kernel(const Params p) {
       // Plain step: both column blocks entirely left (j - i <= -64) or both
       // entirely right (j - i >= 8) of the window, and not the first or the
       // masked step.
-      const int k0 = (w + kWaves * u) * kStep;
-      const bool both_left = k0 + (kStep - 1) - q0 <= -kLeft;
-      const bool both_right = k0 - (q0 + 63) >= kRight;
-      const bool plain = u > 0 && (both_left || both_right) && k0 + kStep <= LK;
+      const bool both_left = u <= uL;
+      const bool plain = u > 0 && (both_left || u >= uR) && u < uM;
       const float off0 = both_left ? qr_l[0] : qr_r[0];
       const float off1 = both_left ? qr_l[1] : qr_r[1];
+      const bool k_last = w + kWaves * (u + 2) >= T - 1;
+      const bool v_last = w + kWaves * (u + 1) >= T - 1;
       half_step(
-          u, 0, [&]() { copy_tile(kbase, kstride, koff, koff_last, u + kStages, ring_lds + c0, ragged); },
-          [&]() {
+          u, 0,
+          [&]() SIDON_INLINE {
+            copy_from(k_last ? klast : gk, koff, koff_last, ring_lds + c0, ragged && k_last);
+          },
+          [&]() SIDON_INLINE { pv(0); },
+          [&]() SIDON_INLINE {
             qk(1);
-            pv(0);
             load_k(c1);
           },
           plain, off0);
       half_step(
           u, 1,
-          [&]() {
-            copy_tile(vbase, vstride, voff, voff_last, u + kStages - 1,
-                      ring_lds + kVRing + (kStages == 3 ? c2 : c1), ragged);
+          [&]() SIDON_INLINE {
+            copy_from(v_last ? vlast : gv, voff, voff_last, ring_lds + kVRing + c1, ragged && v_last);
           },
-          [&]() {
-            pv(1);
+          [&]() SIDON_INLINE { pv(1); },
+          [&]() SIDON_INLINE {
             qk(0);
             load_v(c0);
           },
           plain, off1);
       const uint32_t c = c0;
       c0 = c1;
-      if (kStages == 3) {
-        c1 = c2;
-        c2 = c;
-      } else {
-        c1 = c;
-      }
+      c1 = c;
+      gk += kinc;
+      gv += vinc;
     }
     __builtin_amdgcn_s_setprio(0);
     settle(nu - 1, 1);
