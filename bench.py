@@ -8,6 +8,7 @@ stream before layer l+1 (computed once, untimed: the inputs of every layer
 are resident in HBM before timing starts).  Prints ONE JSON line on stdout.
 
     python bench.py [--steps K] [--warmup W] [--no-cpu-baseline] [--no-check]
+    python bench.py --workload c4     # bucket sweep: 128 clips, one graph per bucket
 
 Timing follows src/sidon_triton/engines.py:26-44 (warm-up, then events on
 the stream the work runs on).  The CPU baseline is the fp32 torch
@@ -88,6 +89,116 @@ def cpu_baseline(torch, qkv0, rel0, heads):
     }
 
 
+def c4_clips(count=128, rate=16000, source_seconds=64.0):
+    """(L, LK) of the c4 clips: the draw sequence of scripts/bench_e2e.py:137-143
+    (random.Random(0); uniform(1.5, 25) seconds, then the start offset, which
+    is drawn and discarded here), bucketed as L = 50 * ceil(sec) with
+    LK = round(50 * sec) valid frames, sec = int(s * rate) / rate."""
+    import random
+    rng = random.Random(0)
+    source_len = int(source_seconds * rate)
+    clips = []
+    for _ in range(count):
+        s = rng.uniform(1.5, 25.0)
+        rng.randint(0, source_len - int(s * rate) - 1)
+        sec = int(s * rate) / rate
+        clips.append((50 * math.ceil(sec), int(round(50 * sec))))
+    return clips
+
+
+def run_c4(torch, sidon, args) -> dict:
+    """128 clips, batch 1 each, 8 layers of attention per clip; one graph per
+    bucket (L) that reads the clip's LK from a device buffer set before each
+    replay.  Inputs per bucket: seeded fp16 q/k/v ~N(0,1) per layer and the
+    per-layer tables of c3."""
+    dev = torch.device("cuda:0")
+    clips = c4_clips()
+    buckets = sorted({L for L, _ in clips})
+    _, rels, _ = build_inputs(torch)
+    rels_d = [r.to(dev) for r in rels]
+    attn = sidon.encoder_attention.flexrel_attention
+    graphs = sidon.graphs.BucketGraphs()
+    state = {}
+    for L in buckets:
+        gen = torch.Generator().manual_seed(1000 + L)
+        qkv = [torch.randn(L, 3 * H * D, generator=gen).half().to(dev) for _ in range(LAYERS)]
+        outs = [torch.empty(L, H * D, dtype=torch.float16, device=dev) for _ in range(LAYERS)]
+        lens = torch.full((1,), L, dtype=torch.int32, device=dev)
+
+        def enqueue(qkv=qkv, outs=outs, lens=lens):
+            for i in range(LAYERS):
+                attn(qkv[i], 1, H, rels_d[i], lens, out=outs[i])
+        state[L] = (qkv, outs, lens, graphs.capture(("c4", L), enqueue))
+    lens_all = torch.tensor([lk for _, lk in clips], dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream()
+
+    def run_all():
+        for j, (L, _) in enumerate(clips):
+            _, _, lens, graph = state[L]
+            lens.copy_(lens_all[j:j + 1])
+            graph.replay()
+    for _ in range(max(1, args.warmup // 2)):
+        run_all()
+    torch.cuda.synchronize()
+    totals = []
+    for _ in range(3):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        run_all()
+        e1.record(stream)
+        e1.synchronize()
+        totals.append(e0.elapsed_time(e1))
+    total_ms = statistics.median(totals)
+    # per bucket: each clip's replay timed on its own (median over 5 repeats)
+    per = {}
+    for j, (L, lk) in enumerate(clips):
+        _, _, lens, graph = state[L]
+        lens.copy_(lens_all[j:j + 1])
+        samples = []
+        for _ in range(5):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            graph.replay()
+            e1.record(stream)
+            e1.synchronize()
+            samples.append(e0.elapsed_time(e1))
+        per.setdefault(L, []).append((lk, statistics.median(samples)))
+    rows = []
+    flops_total = 0.0
+    for L in buckets:
+        fl = sum(LAYERS * attention_flops(H, lk, lk) for lk, _ in per[L])
+        ms = sum(t for _, t in per[L])
+        flops_total += fl
+        rows.append({"L": L, "clips": len(per[L]), "ms_per_clip": ms / len(per[L]),
+                     "tflops": fl / (ms * 1e-3) / 1e12})
+    check = {}
+    if not args.no_check:
+        from oracle.flexrel_oracle import errors, flexrel_reference
+        for j in (0, 1, 2):
+            L, lk = clips[j]
+            qkv, outs, lens, graph = state[L]
+            lens.copy_(lens_all[j:j + 1])
+            graph.replay()
+            torch.cuda.synchronize()
+            view = qkv[0].view(1, L, 3, H, D).float().cpu().numpy()
+            q, k, v = (view[:, :lk, i, [0, 15]].transpose(0, 2, 1, 3) for i in range(3))
+            ref = flexrel_reference(q, k, v, rels[0].float().numpy())
+            got = outs[0].view(1, L, H, D)[:, :lk, [0, 15]].permute(0, 2, 1, 3).float().cpu().numpy()
+            check[f"clip{j}_L{L}_LK{lk}"] = errors(ref, got)
+            log(f"parity c4 clip {j} (L={L}, LK={lk}, layer 0, heads 0/15): {check[f'clip{j}_L{L}_LK{lk}']}")
+    audio = sum(lk for _, lk in clips) / 50.0
+    return {
+        "metric": "ms for 128 bucketed clips (8-layer attn per clip, graph per bucket)",
+        "value": total_ms, "unit": "ms", "n_gpus": 1, "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
+        "data": "synthetic (seeded fp16 q/k/v ~N(0,1) per bucket and layer; c3 tables); clip lengths from random.Random(0) as scripts/bench_e2e.py:137-143",
+        "config": {"workload": "c4: 128 clips, uniform 1.5-25 s, L = 50 ceil(s), LK = round(50 s), batch 1, H=16, D=64, 8 layers",
+                   "buckets": len(buckets), "audio_seconds": audio},
+        "tflops_aggregate": flops_total / (total_ms * 1e-3) / 1e12,
+        "per_bucket": rows, "check": check,
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -97,6 +208,7 @@ def main() -> int:
     ap.add_argument("--cpu-heads", type=int, default=4)
     ap.add_argument("--no-check", action="store_true")
     ap.add_argument("--no-projections", action="store_true")
+    ap.add_argument("--workload", choices=["c3", "c4"], default="c3")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run 3 plain device copies of 256 MiB (calibrates the HBM byte counters)")
     args = ap.parse_args()
@@ -121,6 +233,9 @@ def main() -> int:
     sidon = load_package()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.workload == "c4":
+        print(json.dumps(run_c4(torch, sidon, args)), flush=True)
+        return 0
     shape = sidon._lib.launch_shape(B, H, L)
     log(f"launch shape at L={L}: {shape}; {sidon._lib.version()}")
 
