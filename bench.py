@@ -9,6 +9,7 @@ are resident in HBM before timing starts).  Prints ONE JSON line on stdout.
 
     python bench.py [--steps K] [--warmup W] [--no-cpu-baseline] [--no-check]
     python bench.py --workload c4     # bucket sweep: 128 clips, one graph per bucket
+    python bench.py --workload c5     # conformer attention sub-block, 8 layers
 
 Timing follows src/sidon_triton/engines.py:26-44 (warm-up, then events on
 the stream the work runs on).  The CPU baseline is the fp32 torch
@@ -171,21 +172,6 @@ def run_c4(torch, sidon, args) -> dict:
         flops_total += fl
         rows.append({"L": L, "clips": len(per[L]), "ms_per_clip": ms / len(per[L]),
                      "tflops": fl / (ms * 1e-3) / 1e12})
-    check = {}
-    if not args.no_check:
-        from oracle.flexrel_oracle import errors, flexrel_reference
-        for j in (0, 1, 2):
-            L, lk = clips[j]
-            qkv, outs, lens, graph = state[L]
-            lens.copy_(lens_all[j:j + 1])
-            graph.replay()
-            torch.cuda.synchronize()
-            view = qkv[0].view(1, L, 3, H, D).float().cpu().numpy()
-            q, k, v = (view[:, :lk, i, [0, 15]].transpose(0, 2, 1, 3) for i in range(3))
-            ref = flexrel_reference(q, k, v, rels[0].float().numpy())
-            got = outs[0].view(1, L, H, D)[:, :lk, [0, 15]].permute(0, 2, 1, 3).float().cpu().numpy()
-            check[f"clip{j}_L{L}_LK{lk}"] = errors(ref, got)
-            log(f"parity c4 clip {j} (L={L}, LK={lk}, layer 0, heads 0/15): {check[f'clip{j}_L{L}_LK{lk}']}")
     audio = sum(lk for _, lk in clips) / 50.0
     return {
         "metric": "ms for 128 bucketed clips (8-layer attn per clip, graph per bucket)",
@@ -195,8 +181,80 @@ def run_c4(torch, sidon, args) -> dict:
         "config": {"workload": "c4: 128 clips, uniform 1.5-25 s, L = 50 ceil(s), LK = round(50 s), batch 1, H=16, D=64, 8 layers",
                    "buckets": len(buckets), "audio_seconds": audio},
         "tflops_aggregate": flops_total / (total_ms * 1e-3) / 1e12,
-        "per_bucket": rows, "check": check,
+        "per_bucket": rows,
     }
+
+
+def c5_inputs(torch, seed=5):
+    """Seeded c5 inputs: the fp32 stream [L, 1024] ~N(0,1) and per layer the
+    LayerNorm (w ~1+N(0,.02), b ~N(0,.02), eps 1e-5), fused QKV weight and bias
+    (fp16 ~N(0,.02)), the c3 table, out-projection weight (fp16 ~N(0,.02)) and
+    bias (fp32 ~N(0,.02))."""
+    hid = H * D
+    gen = torch.Generator().manual_seed(seed)
+    x0 = torch.randn(B * L, hid, generator=gen)
+    _, rels, _ = build_inputs(torch)
+    raw = []
+    for i in range(LAYERS):
+        raw.append({
+            "attn_ln": (1.0 + 0.02 * torch.randn(hid, generator=gen), 0.02 * torch.randn(hid, generator=gen), 1e-5),
+            "qkv_w": (torch.randn(3 * hid, hid, generator=gen) * 0.02).half(),
+            "qkv_b": (torch.randn(3 * hid, generator=gen) * 0.02).half(),
+            "rel": rels[i],
+            "out_w": (torch.randn(hid, hid, generator=gen) * 0.02).half(),
+            "out_b": torch.randn(hid, generator=gen) * 0.02,
+        })
+    return x0, raw
+
+
+def run_c5(torch, sidon, args) -> dict:
+    """8 conformer attention sub-blocks on the fp32 residual stream [4800, 1024]:
+    res_norm (LN) -> fused QKV GEMM (fp16, hipBLASLt) -> this attention ->
+    out-projection accumulated in fp32 into the stream (running bias in the
+    next norm), one HIP graph.  Parity at this size is
+    tests/test_block_gpu.py::test_c5_chunk_matches_fp32_torch."""
+    dev = torch.device("cuda:0")
+    hid = H * D
+    x0, raw = c5_inputs(torch)
+    cum = sidon.encoder_block.running_biases([p["out_b"] for p in raw])
+    layers = [{"attn_ln": tuple(t.to(dev) if torch.is_tensor(t) else t for t in p["attn_ln"]),
+               "qkv_w": p["qkv_w"].to(dev), "qkv_b": p["qkv_b"].to(dev), "rel": p["rel"].to(dev),
+               "out_w": p["out_w"].to(dev), "cum_bias": c.to(dev)} for p, c in zip(raw, cum)]
+    bufs = {"xn": torch.empty(B * L, hid, dtype=torch.float16, device=dev),
+            "qkv": torch.empty(B * L, 3 * hid, dtype=torch.float16, device=dev),
+            "ctx": torch.empty(B * L, hid, dtype=torch.float16, device=dev)}
+    lens = torch.full((B,), L, dtype=torch.int32, device=dev)
+    x0_d = x0.to(dev)
+    x = torch.empty_like(x0_d)
+
+    def enqueue():
+        x.copy_(x0_d)
+        sidon.encoder_block.attention_blocks(x, layers, B, H, lens, bufs)
+    graph = sidon.graphs.BucketGraphs().capture(("c5", L), enqueue)
+    stream = torch.cuda.current_stream()
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    steps = max(1, args.steps)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        graph.replay()
+    e1.record(stream)
+    e1.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    gemm_flops = LAYERS * 2.0 * B * L * hid * (3 * hid + hid)
+    attn_flops = LAYERS * attention_flops(B * H, L, L)
+    result = {
+        "metric": "ms per 96 s chunk (8 conformer attention sub-blocks, L=4800)",
+        "value": ms, "unit": "ms", "n_gpus": 1, "steps": steps, "warmup": args.warmup,
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
+        "data": "synthetic (seeded fp32 stream ~N(0,1); LN w ~1+N(0,.02); fp16 QKV / out weights ~N(0,.02); c3 tables)",
+        "config": {"workload": "c5: res_norm -> fused QKV GEMM -> relative_key attention -> out-proj into fp32 stream, x8",
+                   "batch": B, "seq_len": L, "hidden": hid, "heads": H, "layers": LAYERS},
+        "tflops": (gemm_flops + attn_flops) / (ms * 1e-3) / 1e12,
+    }
+    return result
 
 
 def main() -> int:
@@ -206,9 +264,11 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-heads", type=int, default=4)
-    ap.add_argument("--no-check", action="store_true")
+    ap.add_argument("--no-check", action="store_true",
+                    help="accepted for compatibility; parity is checked by tests/ (the oracle is used here only "
+                         "for the CPU baseline)")
     ap.add_argument("--no-projections", action="store_true")
-    ap.add_argument("--workload", choices=["c3", "c4"], default="c3")
+    ap.add_argument("--workload", choices=["c3", "c4", "c5"], default="c3")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run 3 plain device copies of 256 MiB (calibrates the HBM byte counters)")
     args = ap.parse_args()
@@ -235,6 +295,9 @@ def main() -> int:
     torch.cuda.set_device(dev)
     if args.workload == "c4":
         print(json.dumps(run_c4(torch, sidon, args)), flush=True)
+        return 0
+    if args.workload == "c5":
+        print(json.dumps(run_c5(torch, sidon, args)), flush=True)
         return 0
     shape = sidon._lib.launch_shape(B, H, L)
     log(f"launch shape at L={L}: {shape}; {sidon._lib.version()}")
@@ -318,18 +381,6 @@ def main() -> int:
         c1.record(stream)
         c1.synchronize()
         extra["with_projections_ms"] = c0.elapsed_time(c1) / 10
-
-    if not args.no_check:
-        from oracle.flexrel_oracle import errors, flexrel_reference
-        heads = [0, 15]
-        for layer in (0, LAYERS - 1):
-            view = qkv[layer].view(B, L, 3, H, D).float().cpu().numpy()
-            q, k, v = (view[:, :, i, heads].transpose(0, 2, 1, 3) for i in range(3))
-            ref = flexrel_reference(q, k, v, rels[layer].float().numpy())
-            got = outs[layer].view(B, L, H, D)[:, :, heads].permute(0, 2, 1, 3).float().cpu().numpy()
-            err = errors(ref, got)
-            extra[f"check_layer{layer}_heads_0_15"] = err
-            log(f"parity (layer {layer}, heads {heads}): {err}")
 
     traffic = None
     if TRAFFIC_FILE.exists():

@@ -225,30 +225,33 @@ def flexrel_tiled(q, k, v, rel, lens=None, rows_per_block: int = 32, keys_per_ti
     return out
 
 
-def torch_core_chunked(q, k, v, rel, lens=None, out=None, chunk: int = 512):
+def torch_core_chunked(q, k, v, rel, lens=None, out=None, chunk: int = 512, dtype=None):
     """fp32 torch restatement of flexrel_triton.py:297-328 with the key mask.
 
     This is the CPU baseline the benchmark times (the reference's own
-    CPU-capable fp32 path); tensors are CPU torch tensors [B, H, L, D].
+    CPU-capable fp32 path); tensors are torch tensors [B, H, L, D] on any
+    device.  ``dtype`` (default float32) is the compute precision.
     """
     import torch
 
     batch, heads, length, dim = q.shape
+    dtype = torch.float32 if dtype is None else dtype
+    dev = q.device
     scale = 1.0 / math.sqrt(dim)
     if out is None:
-        out = torch.zeros(q.shape, dtype=torch.float32)
-    rf = rel.float()
+        out = torch.zeros(q.shape, dtype=dtype, device=dev)
+    rf = rel.to(dtype)
     for b, lk in enumerate(_lens_of(None if lens is None else [int(x) for x in lens], batch, length)):
         if lk == 0:
             out[b].zero_()
             continue
-        kf = k[b:b + 1, :, :lk].float()
-        vf = v[b:b + 1, :, :lk].float()
-        pos_k = torch.arange(lk)
+        kf = k[b:b + 1, :, :lk].to(dtype)
+        vf = v[b:b + 1, :, :lk].to(dtype)
+        pos_k = torch.arange(lk, device=dev)
         for start in range(0, length, chunk):
             stop = min(start + chunk, length)
-            qc = q[b:b + 1, :, start:stop].float()
-            idx = torch.clamp(pos_k[None, :] - torch.arange(start, stop)[:, None], -LEFT, RIGHT) + LEFT
+            qc = q[b:b + 1, :, start:stop].to(dtype)
+            idx = torch.clamp(pos_k[None, :] - torch.arange(start, stop, device=dev)[:, None], -LEFT, RIGHT) + LEFT
             bias = torch.gather(torch.einsum("bhld,rd->bhlr", qc, rf), 3,
                                 idx.view(1, 1, stop - start, lk).expand(1, heads, -1, -1))
             scores = (qc @ kf.transpose(-2, -1) + bias) * scale

@@ -7,13 +7,16 @@ Entry points (same argument meaning as the reference):
   * ``encoder_attention.flexrel_attention(qkv, batch, heads, rel, lens)`` --
     src/sidon_triton/triton_encoder.py:346 (fused QKV rows);
   * ``graphs.BucketGraphs`` -- one HIP graph per length bucket
-    (src/sidon_triton/runtime.py:374-401).
+    (src/sidon_triton/runtime.py:374-401);
+  * ``encoder_block.res_norm`` / ``encoder_block.attention_blocks`` -- the
+    residual LayerNorm and the conformer attention sub-block around the
+    attention (src/sidon_triton/triton_encoder.py:61-100, :491-503).
 
 The package directory name is not a Python identifier; the repository's
 entry scripts load it under the module name ``sidon_triton_amd``.
 """
 
-from . import _lib, encoder_attention, flexrel, graphs
+from . import _lib, encoder_attention, encoder_block, flexrel, graphs
 from .flexrel import HEAD_DIM, LEFT, NUM_POS, RIGHT, flexrel_attention
 
 __all__ = [
@@ -22,6 +25,7 @@ __all__ = [
     "NUM_POS",
     "RIGHT",
     "encoder_attention",
+    "encoder_block",
     "flexrel",
     "flexrel_attention",
     "graphs",

@@ -1,4 +1,5 @@
-"""ctypes binding of libsidon_flexrel.so (the C ABI in include/sidon_flexrel.h).
+"""ctypes binding of libsidon_flexrel.so (the C ABI in include/sidon_flexrel.h and
+include/sidon_encoder.h).
 
 There is no fallback: if the library is missing or fails to load, every entry
 point raises.  The library is built by ``build.py`` (or ``__graft_entry__.build()``).
@@ -21,7 +22,7 @@ ERROR_NAMES = {
     -6: "SIDON_E_DEVICE",
 }
 
-# Every symbol include/sidon_flexrel.h declares, with its ctypes signature.
+# Every symbol include/*.h declares, with its ctypes signature.
 _I64P = ctypes.POINTER(ctypes.c_int64)
 _IP = ctypes.POINTER(ctypes.c_int)
 _VP = ctypes.c_void_p
@@ -32,6 +33,8 @@ SIGNATURES = {
                                              ctypes.c_int, _VP]),
     "sidon_flexrel_launch_shape": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int, _IP, _IP,
                                                   _IP, _IP]),
+    "sidon_res_norm": (ctypes.c_int, [_VP, _VP, _VP, _VP, _VP, ctypes.c_float, ctypes.c_int, _VP, _VP,
+                                      ctypes.c_float, _VP, ctypes.c_int, ctypes.c_int, ctypes.c_int, _VP]),
     "sidon_last_error": (ctypes.c_char_p, []),
     "sidon_version": (ctypes.c_char_p, []),
 }

@@ -61,6 +61,7 @@
 #include <type_traits>
 
 #include "sidon_flexrel.h"
+#include "sidon_host.h"
 
 #define SIDON_API extern "C" __attribute__((visibility("default")))
 // Kernel-body lambdas index register arrays with their arguments; inlined,
@@ -750,17 +751,9 @@ flexrel_fwd_kernel(const Params p) {
 // ---------------------------------------------------------------------------
 // host side
 
-thread_local char g_err[512] = "";
-
-int fail(int code, const char* fmt, ...) {
-  va_list ap;
-  va_start(ap, fmt);
-  vsnprintf(g_err, sizeof(g_err), fmt, ap);
-  va_end(ap);
-  return code;
-}
-
-bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
+using sidon::aligned16;
+using sidon::check_device;
+using sidon::fail;
 
 int check_strides(const char* name, const int64_t* st) {
   if (st == nullptr) return fail(SIDON_E_NULL, "%s_strides is NULL", name);
@@ -774,6 +767,22 @@ int check_strides(const char* name, const int64_t* st) {
                 (long long)st[2]);
   return SIDON_OK;
 }
+
+}  // namespace
+
+namespace sidon {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+void clear_error() { g_err[0] = '\0'; }
 
 // One architecture check per device (gfx950 only).
 int check_device() {
@@ -795,7 +804,7 @@ int check_device() {
   return SIDON_OK;
 }
 
-}  // namespace
+}  // namespace sidon
 
 SIDON_API int sidon_flexrel_launch_shape(int B, int H, int L, int* queries_per_block,
                                          int* key_splits, int* workgroups, int* threads_per_block) {
@@ -815,7 +824,7 @@ SIDON_API int sidon_flexrel_fwd(const void* q, const void* k, const void* v, con
                                 const int64_t* q_strides, const int64_t* k_strides,
                                 const int64_t* v_strides, const int64_t* o_strides,
                                 sidon_stream_t stream) {
-  g_err[0] = '\0';
+  sidon::clear_error();
   if (!q || !k || !v || !rel || !out) return fail(SIDON_E_NULL, "q, k, v, rel and out must be non-NULL");
   if (head_dim != kD) return fail(SIDON_E_SHAPE, "head_dim must be 64 (got %d)", head_dim);
   if (B < 1 || H < 1 || L < 1) return fail(SIDON_E_SHAPE, "B=%d H=%d L=%d must be >= 1", B, H, L);
@@ -866,7 +875,7 @@ SIDON_API int sidon_flexrel_fwd(const void* q, const void* k, const void* v, con
 
 SIDON_API int sidon_flexrel_fwd_qkv(const void* qkv, const void* rel, const int32_t* lens, void* out,
                                     int B, int H, int L, sidon_stream_t stream) {
-  g_err[0] = '\0';
+  sidon::clear_error();
   if (!qkv || !out || !rel) return fail(SIDON_E_NULL, "qkv, rel and out must be non-NULL");
   if (B < 1 || H < 1 || L < 1) return fail(SIDON_E_SHAPE, "B=%d H=%d L=%d must be >= 1", B, H, L);
   const int64_t hid = (int64_t)H * kD;
@@ -877,6 +886,6 @@ SIDON_API int sidon_flexrel_fwd_qkv(const void* qkv, const void* rel, const int3
                            in_st, in_st, out_st, stream);
 }
 
-SIDON_API const char* sidon_last_error(void) { return g_err; }
+SIDON_API const char* sidon_last_error(void) { return sidon::g_err; }
 
 SIDON_API const char* sidon_version(void) { return "sidon-flexrel 0.2.0 gfx950"; }

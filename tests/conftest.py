@@ -33,7 +33,7 @@ def sidon():
 def golden_cases():
     from make_golden import load_case
 
-    return {p.stem: load_case(p) for p in sorted(GOLDEN.glob("*.npz"))}
+    return {p.stem: load_case(p) for p in sorted(GOLDEN.glob("hf_*.npz"))}
 
 
 def seeded_inputs(batch, heads, length, seed, dtype=np.float16, scale=1.0, rel_std=0.02):
