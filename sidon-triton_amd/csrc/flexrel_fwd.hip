@@ -278,12 +278,6 @@ flexrel_fwd_kernel(const Params p) {
     dma_tile(slot, gb, straddle ? off_last[0] : off[0], straddle ? off_last[1] : off[1],
              straddle ? off_last[2] : off[2], straddle ? off_last[3] : off[3]);
   };
-  // Copy of a tile from gb (its first row, minus 3072) into an LDS slot.
-  auto copy_from = [&](const char* gb, const uint32_t (&off)[4], const uint32_t (&off_last)[4], uint32_t slot,
-                       bool straddle) SIDON_INLINE {
-    dma_tile(slot, gb, straddle ? off_last[0] : off[0], straddle ? off_last[1] : off[1],
-             straddle ? off_last[2] : off[2], straddle ? off_last[3] : off[3]);
-  };
   // Ring slots: K(u) and V(u) live in slot u % 2 of their halves of the ring.
   constexpr uint32_t kVRing = kStages * kTile;
 
@@ -625,7 +619,7 @@ flexrel_fwd_kernel(const Params p) {
     const int uM = ((LK - kStep - kStep * w) >> 8) + 1;
     // Tile sources, advanced by 8 steps per step of this wavefront; copies
     // of step T - 1 (the last one, also for prefetches past the range) read
-    // from klast / vlast with the straddle offsets.
+    // from klast / vlast.
     const int64_t kinc = (int64_t)kWaves * kStep * kstride;
     const int64_t vinc = (int64_t)kWaves * kStep * vstride;
     const char* gk = kbase + (int64_t)(w + 2 * kWaves) * kStep * kstride - 3072;  // K(2)
@@ -633,6 +627,15 @@ flexrel_fwd_kernel(const Params p) {
     const char* klast = kbase + (int64_t)(T - 1) * kStep * kstride - 3072;
     const char* vlast = vbase + (int64_t)(T - 1) * kStep * vstride - 3072;
     uint32_t c0 = 0, c1 = kTile;
+    // Lane offsets of the next copies: the plain ones, switched once (for K
+    // and V separately) to the clamped ones when the copies reach step T - 1
+    // of a ragged LK -- no per-copy select.
+    uint32_t kcur[4], vcur[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      kcur[i] = koff[i];
+      vcur[i] = voff[i];
+    }
     for (int u = 0; u < nu; ++u) {
       // Wavefronts w and w + 4 share a SIMD, and the issue arbiter favours
       // the older one; alternate the wave priority per step so both finish
@@ -651,10 +654,18 @@ flexrel_fwd_kernel(const Params p) {
       const float off1 = both_left ? qr_l[1] : qr_r[1];
       const bool k_last = w + kWaves * (u + 2) >= T - 1;
       const bool v_last = w + kWaves * (u + 1) >= T - 1;
+      if (ragged && k_last) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) kcur[i] = koff_last[i];
+      }
+      if (ragged && v_last) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) vcur[i] = voff_last[i];
+      }
       half_step(
           u, 0,
           [&]() SIDON_INLINE {
-            copy_from(k_last ? klast : gk, koff, koff_last, ring_lds + c0, ragged && k_last);
+            dma_tile(ring_lds + c0, k_last ? klast : gk, kcur[0], kcur[1], kcur[2], kcur[3]);
           },
           [&]() SIDON_INLINE { pv(0); },
           [&]() SIDON_INLINE {
@@ -665,7 +676,7 @@ flexrel_fwd_kernel(const Params p) {
       half_step(
           u, 1,
           [&]() SIDON_INLINE {
-            copy_from(v_last ? vlast : gv, voff, voff_last, ring_lds + kVRing + c1, ragged && v_last);
+            dma_tile(ring_lds + kVRing + c1, v_last ? vlast : gv, vcur[0], vcur[1], vcur[2], vcur[3]);
           },
           [&]() SIDON_INLINE { pv(1); },
           [&]() SIDON_INLINE {
