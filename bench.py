@@ -10,6 +10,7 @@ are resident in HBM before timing starts).  Prints ONE JSON line on stdout.
     python bench.py [--steps K] [--warmup W] [--no-cpu-baseline] [--no-check]
     python bench.py --workload c4     # bucket sweep: 128 clips, one graph per bucket
     python bench.py --workload c5     # conformer attention sub-block, 8 layers
+    python bench.py --workload encoder  # the whole 8-layer conformer encoder
 
 Timing follows src/sidon_triton/engines.py:26-44 (warm-up, then events on
 the stream the work runs on).  The CPU baseline is the fp32 torch
@@ -257,6 +258,95 @@ def run_c5(torch, sidon, args) -> dict:
     return result
 
 
+ENC_FEATURES = 160      # fbank features per 50 Hz frame
+ENC_INTER = 4096        # FFN width
+ENC_KERNEL = 31         # depthwise conv taps
+ENC_H100_MS = 7.6       # encoder stage, 96 s chunk, H100 SXM (reference README.md:40)
+
+
+def encoder_model_weights(torch, seed=7, heads=H, layers=LAYERS, inter=ENC_INTER, kernel=ENC_KERNEL, device="cpu"):
+    """Random-init weights of Sidon's encoder architecture (w2v-BERT 2.0
+    truncated to 8 layers: hidden 1024, 16 heads, FFN 4096, K = 31,
+    tools/convert_torchscript.py:42-68) in the model layout the oracle and
+    ``encoder.pack_weights`` take: LayerNorms w ~1+N(0,.1), b ~N(0,.1);
+    projection weights and biases ~N(0,.02^2); depthwise taps ~N(0,.1^2);
+    tables ~N(0,.02^2).  fp32."""
+    hid = heads * D
+    gen = torch.Generator(device=device).manual_seed(seed)
+
+    def t(*shape, s):
+        return torch.randn(*shape, generator=gen, device=device) * s
+
+    def ln(n):
+        return (1.0 + t(n, s=0.1), t(n, s=0.1), 1e-5)
+
+    weights = {"heads": heads, "fp_ln": ln(ENC_FEATURES), "fp_w": t(hid, ENC_FEATURES, s=0.02),
+               "fp_b": t(hid, s=0.02), "layers": []}
+    for _ in range(layers):
+        p = {"ffn1_ln": ln(hid), "ffn1_w1": t(inter, hid, s=0.02), "ffn1_b1": t(inter, s=0.02),
+             "ffn1_w2": t(hid, inter, s=0.02), "ffn1_b2": t(hid, s=0.02), "attn_ln": ln(hid)}
+        for name in "qkv":
+            p[f"{name}_w"], p[f"{name}_b"] = t(hid, hid, s=0.02), t(hid, s=0.02)
+        p.update({"rel": t(73, D, s=0.02), "out_w": t(hid, hid, s=0.02), "out_b": t(hid, s=0.02),
+                  "conv_ln": ln(hid), "pw1_w": t(2 * hid, hid, s=0.02), "dw_w": t(hid, kernel, s=0.1),
+                  "dw_ln": ln(hid), "pw2_w": t(hid, hid, s=0.02), "ffn2_ln": ln(hid),
+                  "ffn2_w1": t(inter, hid, s=0.02), "ffn2_b1": t(inter, s=0.02), "ffn2_w2": t(hid, inter, s=0.02),
+                  "ffn2_b2": t(hid, s=0.02), "final_ln": ln(hid)})
+        weights["layers"].append(p)
+    return weights
+
+
+def encoder_flops(length, batch=1, heads=H, layers=LAYERS, inter=ENC_INTER, kernel=ENC_KERNEL):
+    """GEMM + attention + depthwise-conv FLOPs of one encoder call (norms and
+    activations not counted)."""
+    hid = heads * D
+    rows = batch * length
+    gemm = 2.0 * rows * (ENC_FEATURES * hid + layers * (2 * 2 * hid * inter + 4 * hid * hid + 2 * hid * hid
+                                                          + hid * hid))
+    conv = layers * 2.0 * rows * hid * kernel
+    return gemm + conv + layers * attention_flops(batch * heads, length, length)
+
+
+def run_encoder(torch, sidon, args) -> dict:
+    """The whole 8-layer conformer encoder on one 96 s chunk (features
+    [1, 4800, 160] -> hidden [1, 4800, 1024]), one HIP graph.  Parity is
+    tests/test_encoder_gpu.py."""
+    dev = torch.device("cuda:0")
+    packed = sidon.encoder.pack_weights(encoder_model_weights(torch))
+    enc = sidon.encoder.HipEncoder(packed, dev)
+    gen = torch.Generator().manual_seed(8)
+    feats = torch.randn(B, L, ENC_FEATURES, generator=gen).to(dev)
+    lens = torch.full((B,), L, dtype=torch.int32, device=dev)
+    out = torch.empty(B, L, enc.hidden, device=dev)
+    ws = enc.workspace(B * L)
+    graph = sidon.graphs.BucketGraphs().capture(("encoder", L), lambda: enc(feats, lens, out=out, workspace=ws))
+    stream = torch.cuda.current_stream()
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    steps = max(1, args.steps)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        graph.replay()
+    e1.record(stream)
+    e1.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    return {
+        "metric": "ms per 96 s chunk (8-layer conformer encoder, L=4800)",
+        "value": ms, "unit": "ms", "n_gpus": 1, "steps": steps, "warmup": args.warmup,
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": ENC_H100_MS / ms,
+        "vs_baseline_note": "speed-up over the reference's published encoder stage, 7.6 ms per 96 s chunk on "
+                            "H100 SXM (README.md:40)",
+        "dtype": "fp16",
+        "data": "synthetic (features ~N(0,1); random-init weights of the architecture, see encoder_model_weights)",
+        "config": {"workload": "encoder: feature projection + 8 conformer layers (FFN, attention, conv, FFN)",
+                   "batch": B, "seq_len": L, "hidden": enc.hidden, "heads": H, "ffn": ENC_INTER,
+                   "conv_kernel": ENC_KERNEL, "layers": LAYERS},
+        "tflops": encoder_flops(L) / (ms * 1e-3) / 1e12,
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -268,7 +358,7 @@ def main() -> int:
                     help="accepted for compatibility; parity is checked by tests/ (the oracle is used here only "
                          "for the CPU baseline)")
     ap.add_argument("--no-projections", action="store_true")
-    ap.add_argument("--workload", choices=["c3", "c4", "c5"], default="c3")
+    ap.add_argument("--workload", choices=["c3", "c4", "c5", "encoder"], default="c3")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run 3 plain device copies of 256 MiB (calibrates the HBM byte counters)")
     args = ap.parse_args()
@@ -295,6 +385,9 @@ def main() -> int:
     torch.cuda.set_device(dev)
     if args.workload == "c4":
         print(json.dumps(run_c4(torch, sidon, args)), flush=True)
+        return 0
+    if args.workload == "encoder":
+        print(json.dumps(run_encoder(torch, sidon, args)), flush=True)
         return 0
     if args.workload == "c5":
         print(json.dumps(run_c5(torch, sidon, args)), flush=True)

@@ -10,13 +10,20 @@ Entry points (same argument meaning as the reference):
     (src/sidon_triton/runtime.py:374-401);
   * ``encoder_block.res_norm`` / ``encoder_block.attention_blocks`` -- the
     residual LayerNorm and the conformer attention sub-block around the
-    attention (src/sidon_triton/triton_encoder.py:61-100, :491-503).
+    attention (src/sidon_triton/triton_encoder.py:61-100, :491-503);
+  * ``conformer.glu`` / ``conformer.causal_dw_norm`` / ``conformer.silu_`` --
+    the conv module's and feed-forward's kernels (triton_encoder.py:113-181);
+  * ``encoder.pack_encoder`` / ``encoder.HipEncoder`` / ``encoder.save_encoder``
+    / ``encoder.load_encoder`` -- the whole 8-layer conformer encoder
+    (triton_encoder.py:392-525);
+  * ``runtime.EncoderRuntime`` -- bucketed, graph-captured encoder calls on
+    fixed max-size buffers (src/sidon_triton/runtime.py:74-186, :366-401).
 
 The package directory name is not a Python identifier; the repository's
 entry scripts load it under the module name ``sidon_triton_amd``.
 """
 
-from . import _lib, encoder_attention, encoder_block, flexrel, graphs
+from . import _lib, conformer, encoder, encoder_attention, encoder_block, flexrel, graphs, runtime
 from .flexrel import HEAD_DIM, LEFT, NUM_POS, RIGHT, flexrel_attention
 
 __all__ = [
@@ -24,10 +31,13 @@ __all__ = [
     "LEFT",
     "NUM_POS",
     "RIGHT",
+    "conformer",
+    "encoder",
     "encoder_attention",
     "encoder_block",
     "flexrel",
     "flexrel_attention",
     "graphs",
+    "runtime",
     "_lib",
 ]

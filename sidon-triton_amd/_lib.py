@@ -35,6 +35,10 @@ SIGNATURES = {
                                                   _IP, _IP]),
     "sidon_res_norm": (ctypes.c_int, [_VP, _VP, _VP, _VP, _VP, ctypes.c_float, ctypes.c_int, _VP, _VP,
                                       ctypes.c_float, _VP, ctypes.c_int, ctypes.c_int, ctypes.c_int, _VP]),
+    "sidon_glu": (ctypes.c_int, [_VP, _VP, ctypes.c_int, ctypes.c_int, _VP]),
+    "sidon_silu": (ctypes.c_int, [_VP, ctypes.c_int64, _VP]),
+    "sidon_causal_dw_norm": (ctypes.c_int, [_VP, ctypes.c_int, _VP, _VP, _VP, ctypes.c_float, _VP,
+                                            ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _VP]),
     "sidon_last_error": (ctypes.c_char_p, []),
     "sidon_version": (ctypes.c_char_p, []),
 }

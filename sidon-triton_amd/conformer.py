@@ -1,0 +1,108 @@
+"""The conformer layer's elementwise and convolution ops on the MI355X library.
+
+Same names and argument meaning as src/sidon_triton/triton_encoder.py:
+
+  * ``glu(h)`` (:127-133): h [R, 2C] fp16 -> h[:, :C] * sigmoid(h[:, C:]) fp16;
+  * ``causal_dw_norm(g, batch, dwt, ln_w, ln_b, eps)`` (:163-181): g [B*T, C]
+    fp16, dwt [K, C] fp32 -> silu(LN(causal depthwise conv)) fp16;
+  * ``silu_(h)``: the in-place F.silu of the feed-forward modules (:485-486);
+
+plus ``glu_causal_dw_norm(h, ...)``, the two fused: it reads the pointwise
+conv's output h [B*T, 2C] and forms g on the fly (bit-identical to
+``causal_dw_norm(glu(h), ...)``, without the g round trip through HBM).
+
+All launch on the current stream of the tensors' device through the C ABI of
+include/sidon_encoder.h (csrc/conformer_ops.hip) and allocate only their
+outputs (none when ``out`` is given), so they can be captured into HIP graphs.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+from .flexrel import _check_device_tensor, _stream_handle
+
+
+def _fp16_rows(name, t, device, cols=None):
+    _check_device_tensor(name, t, device)
+    if t.dtype != torch.float16 or t.dim() != 2 or not t.is_contiguous():
+        raise ValueError(f"{name} must be a contiguous float16 [R, C] tensor")
+    if cols is not None and t.shape[1] != cols:
+        raise ValueError(f"{name} must have {cols} columns (got {t.shape[1]})")
+
+
+def glu(h: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    rows, c2 = h.shape
+    if c2 % 2:
+        raise ValueError("h must have an even number of columns")
+    device = h.device
+    _fp16_rows("h", h, device)
+    c = c2 // 2
+    if out is None:
+        out = torch.empty(rows, c, device=device, dtype=h.dtype)
+    else:
+        _fp16_rows("out", out, device, c)
+    lib = _lib.load()
+    with torch.cuda.device(device):
+        rc = lib.sidon_glu(h.data_ptr(), out.data_ptr(), rows, c, _stream_handle(device))
+    _lib.check("sidon_glu", rc)
+    return out
+
+
+def silu_(h: torch.Tensor) -> torch.Tensor:
+    """h = h * sigmoid(h) in place (fp16, any shape, contiguous)."""
+    device = h.device
+    _check_device_tensor("h", h, device)
+    if h.dtype != torch.float16 or not h.is_contiguous():
+        raise ValueError("h must be a contiguous float16 tensor")
+    lib = _lib.load()
+    with torch.cuda.device(device):
+        rc = lib.sidon_silu(h.data_ptr(), h.numel(), _stream_handle(device))
+    _lib.check("sidon_silu", rc)
+    return h
+
+
+def _dw(src, glu_input, batch, dwt, ln_w, ln_b, eps, out):
+    rows, width = src.shape
+    c = width // 2 if glu_input else width
+    device = src.device
+    _fp16_rows("h" if glu_input else "g", src, device)
+    if rows % batch:
+        raise ValueError(f"{rows} rows do not split into {batch} items")
+    for name, t, shape in (("dwt", dwt, None), ("ln_w", ln_w, (c,)), ("ln_b", ln_b, (c,))):
+        _check_device_tensor(name, t, device)
+        if t.dtype != torch.float32 or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous float32 tensor")
+        if shape is not None and tuple(t.shape) != shape:
+            raise ValueError(f"{name} must be [{c}]")
+    if dwt.dim() != 2 or dwt.shape[1] != c:
+        raise ValueError(f"dwt must be [K, {c}]")
+    if out is None:
+        out = torch.empty(rows, c, device=device, dtype=torch.float16)
+    else:
+        _fp16_rows("out", out, device, c)
+        if out.shape[0] != rows:
+            raise ValueError("out must have the input's rows")
+    lib = _lib.load()
+    with torch.cuda.device(device):
+        rc = lib.sidon_causal_dw_norm(src.data_ptr(), int(glu_input), dwt.data_ptr(), ln_w.data_ptr(),
+                                      ln_b.data_ptr(), ctypes.c_float(float(eps)), out.data_ptr(), batch,
+                                      rows // batch, c, dwt.shape[0], _stream_handle(device))
+    _lib.check("sidon_causal_dw_norm", rc)
+    return out
+
+
+def causal_dw_norm(g: torch.Tensor, batch: int, dwt: torch.Tensor, ln_w: torch.Tensor, ln_b: torch.Tensor,
+                   eps: float, out: torch.Tensor | None = None) -> torch.Tensor:
+    """g [B*T, C] fp16 -> silu(LN(sum_k dwt[k] * g[t + k - (K-1)])) [B*T, C] fp16
+    (zero left padding per item; dwt [K, C] fp32, ln_w / ln_b [C] fp32)."""
+    return _dw(g, False, batch, dwt, ln_w, ln_b, eps, out)
+
+
+def glu_causal_dw_norm(h: torch.Tensor, batch: int, dwt: torch.Tensor, ln_w: torch.Tensor, ln_b: torch.Tensor,
+                       eps: float, out: torch.Tensor | None = None) -> torch.Tensor:
+    """causal_dw_norm(glu(h), ...) in one pass: h [B*T, 2C] fp16."""
+    return _dw(h, True, batch, dwt, ln_w, ln_b, eps, out)
