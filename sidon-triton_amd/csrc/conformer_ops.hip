@@ -24,8 +24,11 @@
 
 #include <stdint.h>
 
+#include <algorithm>
+
 #include "sidon_encoder.h"
 #include "sidon_host.h"
+#include "sidon_wave.h"
 
 #define SIDON_API extern "C" __attribute__((visibility("default")))
 
@@ -36,11 +39,13 @@ typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f2 __attribute__((ext_vector_type(2)));
 typedef float f8 __attribute__((ext_vector_type(8)));
 
-constexpr int kBT = 16;          // output frames per causal_dw_norm block
 constexpr int kMaxC = 2048;      // channels: one thread per pair, <= 1024 threads
 constexpr int kEwThreads = 256;  // glu / silu block size
+constexpr int kXcds = 8;         // accelerator complex dies of an MI355X
 
-__device__ __forceinline__ float sigmoid(float x) { return 1.f / (1.f + __expf(-x)); }
+// sigmoid(x) = 1 / (1 + e^-x) with the hardware exponential and reciprocal
+// (each within about 1 ulp in fp32; the results are rounded to fp16).
+__device__ __forceinline__ float sigmoid(float x) { return __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
 
 // GLU of one element as glu stores it: the fp32 product rounded to fp32,
 // then to fp16.  The empty asm keeps the compiler from fusing the product and
@@ -114,119 +119,231 @@ struct DwParams {
   _Float16* out;        // [B*T, C]
   float eps;
   int T, C;
+  int vec8;             // C % 8 == 0 and src 16-byte aligned: 8-channel tile loads
 };
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
-}
+using sidon::wave_sum;
 
-// Sums v[t] over the block's threads for every t < kBT (result in every
-// thread).  red holds kBT floats per wavefront.
-__device__ __forceinline__ void block_sums(float (&v)[kBT], float* red, int nwaves) {
+// Sums v[t] over the block's threads for every t < BT (result in every
+// thread).  red holds BT floats per wavefront.
+template <int BT>
+__device__ __forceinline__ void block_sums(float (&v)[BT], float* red, int nwaves) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
 #pragma unroll
-  for (int t = 0; t < kBT; ++t) v[t] = wave_sum(v[t]);
+  for (int t = 0; t < BT; ++t) v[t] = wave_sum(v[t]);
   if (lane == 0) {
 #pragma unroll
-    for (int t = 0; t < kBT; ++t) red[wave * kBT + t] = v[t];
+    for (int t = 0; t < BT; ++t) red[wave * BT + t] = v[t];
   }
   __syncthreads();
 #pragma unroll
-  for (int t = 0; t < kBT; ++t) v[t] = 0.f;
+  for (int t = 0; t < BT; ++t) v[t] = 0.f;
   for (int w = 0; w < nwaves; ++w) {
 #pragma unroll
-    for (int t = 0; t < kBT; ++t) v[t] += red[w * kBT + t];
+    for (int t = 0; t < BT; ++t) v[t] += red[w * BT + t];
   }
   __syncthreads();  // red is reused by the next reduction
 }
 
-template <int K, bool kGlu>
+// One block: output frames [t0, t0 + BT) of one item, all C channels (tiles
+// numbered item-major over a 1-D grid).
+//   1. The block stages g of source frames t0 - (K - 1) .. t0 + BT - 1 in LDS
+//      (fp16, zeros outside [0, T)), every thread loading whole 16-byte
+//      chunks of four rows at a time from clamped (always valid) rows, so
+//      the four rows' loads are in flight together.
+//   2. Thread i owns channels 2i, 2i + 1: its 2 K taps and BT accumulator
+//      pairs sit in registers; it walks the BT + K - 1 staged frames once,
+//      adding frame j into output i through tap k = j - i, so every output
+//      sums its taps in order k = 0 .. K-1.
+//   3. LayerNorm over the C channels of the BT rows (two passes, block
+//      reductions), SiLU, fp16 store.
+template <int K, int BT, bool kGlu>
 __global__ void __launch_bounds__(1024) causal_dw_norm_kernel(const DwParams p) {
-  __shared__ float red[16 * kBT];
-  const int nwaves = blockDim.x >> 6;
-  const int b = blockIdx.y;
-  const int t0 = blockIdx.x * kBT;
-  const int c = 2 * threadIdx.x;
-  const bool on = c < p.C;  // threads past C hold zeros
+  extern __shared__ __attribute__((aligned(16))) char dw_smem[];
+  __shared__ float red[16 * BT];
+  constexpr int kRows = BT + K - 1;
+  _Float16* tile = reinterpret_cast<_Float16*>(dw_smem);  // [kRows][C]
+  const int C = p.C;
+  const int nthreads = blockDim.x;
+  const int nwaves = nthreads >> 6;
+  // Workgroups go to the 8 XCDs round-robin; give each XCD a contiguous run
+  // of tiles, so the K - 1 frames a tile shares with its left neighbour are
+  // usually in the same L2.
+  const int ntiles = (p.T + BT - 1) / BT;
+  const int nblk = gridDim.x;
+  const int xcd = blockIdx.x % kXcds;
+  const int tile_id = xcd * (nblk / kXcds) + min(xcd, nblk % kXcds) + blockIdx.x / kXcds;
+  const int b = tile_id / ntiles;
+  const int t0 = (tile_id - b * ntiles) * BT;
+  const int s0 = t0 - (K - 1);
   const int64_t row0 = (int64_t)b * p.T;
-  const int64_t src_stride = kGlu ? 2 * (int64_t)p.C : (int64_t)p.C;
+  const int64_t src_stride = kGlu ? 2 * (int64_t)C : (int64_t)C;
 
-  f2 w[K];
+  // 1. stage g
+  {
+    const int width = p.vec8 ? 8 : 2;          // channels per chunk
+    const int cpr = C / width;                 // chunks per row
+    const int rpp = nthreads / cpr;            // rows per pass (>= 1: C / 2 <= nthreads)
+    const int r_first = threadIdx.x / cpr;
+    const int cc = (threadIdx.x - r_first * cpr) * width;
+    if (r_first < rpp) {
+      // Four rows per pass: the loads of all four are issued before any is
+      // used (rows past the tile repeat the last one and are not stored).
+      for (int r = r_first; r < kRows; r += 4 * rpp) {
+        if (p.vec8) {
+          h8 a[4], gate[4];
 #pragma unroll
-  for (int k = 0; k < K; ++k) w[k] = on ? *reinterpret_cast<const f2*>(p.dwt + (int64_t)k * p.C + c) : f2{0.f, 0.f};
-
-  f2 acc[kBT];
+          for (int u = 0; u < 4; ++u) {
+            const int sc = min(max(s0 + min(r + u * rpp, kRows - 1), 0), p.T - 1);
+            const _Float16* src = p.src + (row0 + sc) * src_stride + cc;
+            a[u] = *reinterpret_cast<const h8*>(src);
+            if (kGlu) gate[u] = *reinterpret_cast<const h8*>(src + C);
+          }
 #pragma unroll
-  for (int t = 0; t < kBT; ++t) acc[t] = f2{0.f, 0.f};
-
-  // Source frame s = t0 + j - (K - 1) = (t0 + i) + k - (K - 1) feeds output
-  // frame t0 + i through tap k = j - i, for i in [j - (K - 1), j].
+          for (int u = 0; u < 4; ++u) {
+            const int rr = r + u * rpp;
+            if (rr < kRows) {
+              const int s = s0 + rr;
+              h8 g = a[u];
+              if (kGlu) {
 #pragma unroll
-  for (int j = 0; j < kBT + K - 1; ++j) {
-    const int s = t0 + j - (K - 1);
-    f2 gv = {0.f, 0.f};
-    if (on && s >= 0 && s < p.T) {
-      const _Float16* srow = p.src + (row0 + s) * src_stride + c;
-      const h2 a = *reinterpret_cast<const h2*>(srow);
-      if (kGlu) {
-        const h2 gate = *reinterpret_cast<const h2*>(srow + p.C);
-        gv = f2{(float)glu1((float)a[0], (float)gate[0]), (float)glu1((float)a[1], (float)gate[1])};
-      } else {
-        gv = f2{(float)a[0], (float)a[1]};
+                for (int e = 0; e < 8; ++e) g[e] = glu1((float)a[u][e], (float)gate[u][e]);
+              }
+              if (s < 0 || s >= p.T) g = h8{};
+              *reinterpret_cast<h8*>(tile + rr * C + cc) = g;
+            }
+          }
+        } else {
+          h2 a[4], gate[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const int sc = min(max(s0 + min(r + u * rpp, kRows - 1), 0), p.T - 1);
+            const _Float16* src = p.src + (row0 + sc) * src_stride + cc;
+            a[u] = *reinterpret_cast<const h2*>(src);
+            if (kGlu) gate[u] = *reinterpret_cast<const h2*>(src + C);
+          }
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const int rr = r + u * rpp;
+            if (rr < kRows) {
+              const int s = s0 + rr;
+              h2 g = a[u];
+              if (kGlu) g = h2{glu1((float)a[u][0], (float)gate[u][0]), glu1((float)a[u][1], (float)gate[u][1])};
+              if (s < 0 || s >= p.T) g = h2{};
+              *reinterpret_cast<h2*>(tile + rr * C + cc) = g;
+            }
+          }
+        }
       }
     }
+  }
+  __syncthreads();
+
+  // 2. conv
+  const int c = 2 * threadIdx.x;
+  const bool on = c < C;  // threads past C hold zeros
+  f2 w[K];
 #pragma unroll
-    for (int i = 0; i < kBT; ++i) {
-      const int k = j - i;
-      if (k >= 0 && k < K) {
-        acc[i][0] = fmaf(gv[0], w[k][0], acc[i][0]);
-        acc[i][1] = fmaf(gv[1], w[k][1], acc[i][1]);
+  for (int k = 0; k < K; ++k) w[k] = on ? *reinterpret_cast<const f2*>(p.dwt + (int64_t)k * C + c) : f2{0.f, 0.f};
+  f2 acc[BT];
+#pragma unroll
+  for (int t = 0; t < BT; ++t) acc[t] = f2{0.f, 0.f};
+  if (on) {
+#pragma unroll
+    for (int j = 0; j < kRows; ++j) {
+      const h2 gh = *reinterpret_cast<const h2*>(tile + j * C + c);
+      const f2 gv = {(float)gh[0], (float)gh[1]};
+#pragma unroll
+      for (int i = 0; i < BT; ++i) {
+        const int k = j - i;
+        if (k >= 0 && k < K) {
+          acc[i][0] = fmaf(gv[0], w[k][0], acc[i][0]);
+          acc[i][1] = fmaf(gv[1], w[k][1], acc[i][1]);
+        }
       }
     }
   }
 
-  // LayerNorm over the C channels of every row (two passes), then SiLU.
-  float v[kBT];
+  // 3. LayerNorm over the C channels of every row (two passes), then SiLU.
+  float v[BT];
 #pragma unroll
-  for (int t = 0; t < kBT; ++t) v[t] = acc[t][0] + acc[t][1];
-  block_sums(v, red, nwaves);
-  const float inv_c = 1.f / (float)p.C;
+  for (int t = 0; t < BT; ++t) v[t] = acc[t][0] + acc[t][1];
+  block_sums<BT>(v, red, nwaves);
+  const float inv_c = 1.f / (float)C;
 #pragma unroll
-  for (int t = 0; t < kBT; ++t) {
+  for (int t = 0; t < BT; ++t) {
     const float mean = v[t] * inv_c;
     acc[t][0] = on ? acc[t][0] - mean : 0.f;
     acc[t][1] = on ? acc[t][1] - mean : 0.f;
     v[t] = acc[t][0] * acc[t][0] + acc[t][1] * acc[t][1];
   }
-  block_sums(v, red, nwaves);
+  block_sums<BT>(v, red, nwaves);
   if (!on) return;
   const f2 lw = *reinterpret_cast<const f2*>(p.ln_w + c);
   const f2 lb = *reinterpret_cast<const f2*>(p.ln_b + c);
 #pragma unroll
-  for (int t = 0; t < kBT; ++t) {
+  for (int t = 0; t < BT; ++t) {
     if (t0 + t >= p.T) continue;
     const float rstd = rsqrtf(v[t] * inv_c + p.eps);
-    float y0 = acc[t][0] * rstd * lw[0] + lb[0];
-    float y1 = acc[t][1] * rstd * lw[1] + lb[1];
-    y0 = y0 * sigmoid(y0);
-    y1 = y1 * sigmoid(y1);
-    *reinterpret_cast<h2*>(p.out + (row0 + t0 + t) * p.C + c) = h2{(_Float16)y0, (_Float16)y1};
+    const float y0 = acc[t][0] * rstd * lw[0] + lb[0];
+    const float y1 = acc[t][1] * rstd * lw[1] + lb[1];
+    *reinterpret_cast<h2*>(p.out + (row0 + t0 + t) * C + c) = h2{silu1(y0), silu1(y1)};
   }
+}
+
+constexpr int kLdsBudget = 160 * 1024;  // LDS of one CU
+constexpr int kMaxThreadsPerCU = 2048;
+
+int dw_lds_bytes(int bt, int K, int C) { return (bt + K - 1) * C * 2; }
+
+// Frames per block: the candidate that minimises (rounds of blocks over the
+// chip) x (staged frames per block), within the LDS of one CU.
+int pick_bt(int K, int B, int T, int C, int threads) {
+  static const int kCands[] = {20, 16, 8};
+  int best = 0;
+  long best_cost = 0;
+  const int cus = sidon::compute_units();
+  for (int bt : kCands) {
+    const int lds = dw_lds_bytes(bt, K, C) + 16 * bt * 4;
+    if (lds > kLdsBudget) continue;
+    const int per_cu = std::min(kLdsBudget / lds, kMaxThreadsPerCU / threads);
+    const long blocks = (long)((T + bt - 1) / bt) * B;
+    const long slots = (long)cus * std::max(per_cu, 1);
+    const long cost = ((blocks + slots - 1) / slots) * (bt + K - 1);
+    if (best == 0 || cost < best_cost) {
+      best = bt;
+      best_cost = cost;
+    }
+  }
+  return best;
+}
+
+template <int K, int BT>
+hipError_t launch_dw_bt(const DwParams& p, int B, bool glu_input, int threads, hipStream_t stream) {
+  const dim3 grid((unsigned)(((p.T + BT - 1) / BT) * B));
+  const size_t lds = (size_t)dw_lds_bytes(BT, K, p.C);
+  if (glu_input) {
+    auto fn = causal_dw_norm_kernel<K, BT, true>;
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    hipLaunchKernelGGL(fn, grid, dim3(threads), lds, stream, p);
+  } else {
+    auto fn = causal_dw_norm_kernel<K, BT, false>;
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    hipLaunchKernelGGL(fn, grid, dim3(threads), lds, stream, p);
+  }
+  return hipGetLastError();
 }
 
 template <int K>
 hipError_t launch_dw(const DwParams& p, int B, bool glu_input, hipStream_t stream) {
   const int threads = 64 * ((p.C / 2 + 63) / 64);
-  const dim3 grid((p.T + kBT - 1) / kBT, B);
-  if (glu_input) {
-    hipLaunchKernelGGL((causal_dw_norm_kernel<K, true>), grid, dim3(threads), 0, stream, p);
-  } else {
-    hipLaunchKernelGGL((causal_dw_norm_kernel<K, false>), grid, dim3(threads), 0, stream, p);
+  switch (pick_bt(K, B, p.T, p.C, threads)) {
+    case 20: return launch_dw_bt<K, 20>(p, B, glu_input, threads, stream);
+    case 16: return launch_dw_bt<K, 16>(p, B, glu_input, threads, stream);
+    case 8: return launch_dw_bt<K, 8>(p, B, glu_input, threads, stream);
+    default: return hipErrorInvalidConfiguration;
   }
-  return hipGetLastError();
 }
 
 bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
@@ -297,7 +414,8 @@ SIDON_API int sidon_causal_dw_norm(const void* src, int glu_input, const float* 
     return fail(SIDON_E_ALIGN, "fp32 tensors must be 8-byte aligned");
   int rc;
   if ((rc = sidon::check_device())) return rc;
-  const DwParams p{static_cast<const _Float16*>(src), dwt, ln_w, ln_b, static_cast<_Float16*>(out), eps, T, C};
+  const int vec8 = C % 8 == 0 && aligned(src, 16);
+  const DwParams p{static_cast<const _Float16*>(src), dwt, ln_w, ln_b, static_cast<_Float16*>(out), eps, T, C, vec8};
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const bool g = glu_input != 0;
   hipError_t err;

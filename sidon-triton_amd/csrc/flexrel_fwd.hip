@@ -796,23 +796,35 @@ int fail(int code, const char* fmt, ...) {
 void clear_error() { g_err[0] = '\0'; }
 
 // One architecture check per device (gfx950 only).
+namespace {
+constexpr int kMaxDevices = 64;
+std::once_flag g_dev_flags[kMaxDevices];
+int g_dev_status[kMaxDevices];
+int g_dev_cus[kMaxDevices];
+}  // namespace
+
 int check_device() {
-  static std::once_flag flags[64];
-  static int status[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return fail(SIDON_E_DEVICE, "hipGetDevice failed");
-  if (dev < 0 || dev >= 64) return fail(SIDON_E_DEVICE, "device index %d out of range", dev);
-  std::call_once(flags[dev], [dev]() {
+  if (dev < 0 || dev >= kMaxDevices) return fail(SIDON_E_DEVICE, "device index %d out of range", dev);
+  std::call_once(g_dev_flags[dev], [dev]() {
     hipDeviceProp_t prop;
     if (hipGetDeviceProperties(&prop, dev) != hipSuccess) {
-      status[dev] = -1;
+      g_dev_status[dev] = -1;
       return;
     }
-    status[dev] = strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : -2;
+    g_dev_cus[dev] = prop.multiProcessorCount;
+    g_dev_status[dev] = strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : -2;
   });
-  if (status[dev] == -1) return fail(SIDON_E_DEVICE, "hipGetDeviceProperties failed on device %d", dev);
-  if (status[dev] != 1) return fail(SIDON_E_DEVICE, "device %d is not gfx950", dev);
+  if (g_dev_status[dev] == -1) return fail(SIDON_E_DEVICE, "hipGetDeviceProperties failed on device %d", dev);
+  if (g_dev_status[dev] != 1) return fail(SIDON_E_DEVICE, "device %d is not gfx950", dev);
   return SIDON_OK;
+}
+
+int compute_units() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices || g_dev_status[dev] != 1) return 256;
+  return g_dev_cus[dev];
 }
 
 }  // namespace sidon

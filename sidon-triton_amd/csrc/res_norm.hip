@@ -24,6 +24,7 @@
 
 #include "sidon_encoder.h"
 #include "sidon_host.h"
+#include "sidon_wave.h"
 
 #define SIDON_API extern "C" __attribute__((visibility("default")))
 
@@ -49,16 +50,12 @@ struct RNParams {
   int write_x, xn_fp16;
 };
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
-}
+using sidon::wave_sum;
 
-// v <- LN(v) over the row (chunks past C hold 0 and stay 0).
+// v <- LN(v) over the row (chunks past C hold 0 and stay 0; full: C == 256 NC).
 template <int NC>
 __device__ __forceinline__ void layer_norm(f4 (&v)[NC], int lane, int C, const float* w, const float* b,
-                                           float eps) {
+                                           float eps, bool full) {
   float s = 0.f;
 #pragma unroll
   for (int j = 0; j < NC; ++j) s += (v[j][0] + v[j][1]) + (v[j][2] + v[j][3]);
@@ -67,7 +64,7 @@ __device__ __forceinline__ void layer_norm(f4 (&v)[NC], int lane, int C, const f
 #pragma unroll
   for (int j = 0; j < NC; ++j) {
     const int c = 4 * (lane + 64 * j);
-    if (c < C) {
+    if (full || c < C) {
       v[j] -= mean;
       q += (v[j][0] * v[j][0] + v[j][1] * v[j][1]) + (v[j][2] * v[j][2] + v[j][3] * v[j][3]);
     }
@@ -76,7 +73,7 @@ __device__ __forceinline__ void layer_norm(f4 (&v)[NC], int lane, int C, const f
 #pragma unroll
   for (int j = 0; j < NC; ++j) {
     const int c = 4 * (lane + 64 * j);
-    if (c < C) {
+    if (full || c < C) {
       const f4 wv = *reinterpret_cast<const f4*>(w + c);
       const f4 bv = *reinterpret_cast<const f4*>(b + c);
       v[j] = v[j] * rstd * wv + bv;
@@ -84,8 +81,23 @@ __device__ __forceinline__ void layer_norm(f4 (&v)[NC], int lane, int C, const f
   }
 }
 
-template <int NC>
+// Mode bits: a kernel instantiated with kMode >= 0 has its options fixed at
+// compile time (no per-element branches, loads hoisted freely); kMode = -1
+// reads them from the parameters.
+constexpr int kY = 1, kBias = 2, kNorm1 = 4, kWriteX = 8, kNorm2 = 16, kFp16 = 32, kFull = 64;
+constexpr int kModeBiasNorm = kBias | kNorm2 | kFp16 | kFull;                     // x + b -> LN2 (fp16)
+constexpr int kModeFinal = kBias | kNorm1 | kWriteX | kNorm2 | kFp16 | kFull;     // x = LN1(x + b) -> LN2
+
+template <int NC, int kMode>
 __global__ void __launch_bounds__(64 * kRowsPerBlock) res_norm_kernel(const RNParams p) {
+  constexpr bool kFixed = kMode >= 0;
+  const bool has_y = kFixed ? (kMode & kY) != 0 : p.y != nullptr;
+  const bool has_bias = kFixed ? (kMode & kBias) != 0 : p.bias != nullptr;
+  const bool norm1 = kFixed ? (kMode & kNorm1) != 0 : p.n1_w != nullptr;
+  const bool write_x = kFixed ? (kMode & kWriteX) != 0 : p.write_x != 0;
+  const bool norm2 = kFixed ? (kMode & kNorm2) != 0 : p.n2_w != nullptr;
+  const bool fp16 = kFixed ? (kMode & kFp16) != 0 : p.xn_fp16 != 0;
+  const bool full = kFixed && (kMode & kFull) != 0;  // C == 256 NC: every chunk in range
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
   if (row >= p.R) return;
@@ -95,27 +107,27 @@ __global__ void __launch_bounds__(64 * kRowsPerBlock) res_norm_kernel(const RNPa
   for (int j = 0; j < NC; ++j) {
     const int c = 4 * (lane + 64 * j);
     v[j] = f4{0.f, 0.f, 0.f, 0.f};
-    if (c < p.C) {
+    if (full || c < p.C) {
       v[j] = *reinterpret_cast<const f4*>(p.x + base + c);
-      if (p.bias) v[j] += *reinterpret_cast<const f4*>(p.bias + c);
-      if (p.y) v[j] += *reinterpret_cast<const f4*>(p.y + base + c);
+      if (has_bias) v[j] += *reinterpret_cast<const f4*>(p.bias + c);
+      if (has_y) v[j] += *reinterpret_cast<const f4*>(p.y + base + c);
     }
   }
-  if (p.n1_w) layer_norm<NC>(v, lane, p.C, p.n1_w, p.n1_b, p.eps1);
-  if (p.write_x) {
+  if (norm1) layer_norm<NC>(v, lane, p.C, p.n1_w, p.n1_b, p.eps1, full);
+  if (write_x) {
 #pragma unroll
     for (int j = 0; j < NC; ++j) {
       const int c = 4 * (lane + 64 * j);
-      if (c < p.C) *reinterpret_cast<f4*>(p.x + base + c) = v[j];
+      if (full || c < p.C) *reinterpret_cast<f4*>(p.x + base + c) = v[j];
     }
   }
-  if (p.n2_w) {
-    layer_norm<NC>(v, lane, p.C, p.n2_w, p.n2_b, p.eps2);
+  if (norm2) {
+    layer_norm<NC>(v, lane, p.C, p.n2_w, p.n2_b, p.eps2, full);
 #pragma unroll
     for (int j = 0; j < NC; ++j) {
       const int c = 4 * (lane + 64 * j);
-      if (c < p.C) {
-        if (p.xn_fp16) {
+      if (full || c < p.C) {
+        if (fp16) {
           *reinterpret_cast<h4*>(static_cast<_Float16*>(p.xn) + base + c) = __builtin_convertvector(v[j], h4);
         } else {
           *reinterpret_cast<f4*>(static_cast<float*>(p.xn) + base + c) = v[j];
@@ -128,7 +140,15 @@ __global__ void __launch_bounds__(64 * kRowsPerBlock) res_norm_kernel(const RNPa
 template <int NC>
 hipError_t launch(const RNParams& p, hipStream_t stream) {
   const int blocks = (p.R + kRowsPerBlock - 1) / kRowsPerBlock;
-  hipLaunchKernelGGL(res_norm_kernel<NC>, dim3(blocks), dim3(64 * kRowsPerBlock), 0, stream, p);
+  const int mode = (p.y ? kY : 0) | (p.bias ? kBias : 0) | (p.n1_w ? kNorm1 : 0) | (p.write_x ? kWriteX : 0) |
+                   (p.n2_w ? kNorm2 : 0) | (p.xn_fp16 ? kFp16 : 0) | (p.C == 256 * NC ? kFull : 0);
+  if (mode == kModeBiasNorm) {
+    hipLaunchKernelGGL((res_norm_kernel<NC, kModeBiasNorm>), dim3(blocks), dim3(64 * kRowsPerBlock), 0, stream, p);
+  } else if (mode == kModeFinal) {
+    hipLaunchKernelGGL((res_norm_kernel<NC, kModeFinal>), dim3(blocks), dim3(64 * kRowsPerBlock), 0, stream, p);
+  } else {
+    hipLaunchKernelGGL((res_norm_kernel<NC, -1>), dim3(blocks), dim3(64 * kRowsPerBlock), 0, stream, p);
+  }
   return hipGetLastError();
 }
 

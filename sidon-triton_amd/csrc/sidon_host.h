@@ -15,6 +15,8 @@ int fail(int code, const char* fmt, ...);
 void clear_error();
 // SIDON_OK when the current HIP device is a gfx950, else SIDON_E_DEVICE.
 int check_device();
+// Compute units of the current device (after a successful check_device).
+int compute_units();
 
 inline bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
 
