@@ -11,6 +11,7 @@ are resident in HBM before timing starts).  Prints ONE JSON line on stdout.
     python bench.py --workload c4     # bucket sweep: 128 clips, one graph per bucket
     python bench.py --workload c5     # conformer attention sub-block, 8 layers
     python bench.py --workload encoder  # the whole 8-layer conformer encoder
+    python bench.py --workload frontend # the bucket-masked fbank front end
 
 Timing follows src/sidon_triton/engines.py:26-44 (warm-up, then events on
 the stream the work runs on).  The CPU baseline is the fp32 torch
@@ -347,6 +348,50 @@ def run_encoder(torch, sidon, args) -> dict:
     }
 
 
+FE_H100_MS = 0.33       # front end (fbank on GPU) per chunk, H100 (reference README.md:42-43)
+
+
+def run_frontend(torch, sidon, args) -> dict:
+    """The bucket-masked fbank front end on one 96 s chunk (1,536,000 samples
+    -> features [1, 4800, 160]), one HIP graph.  Parity is
+    tests/test_frontend_gpu.py."""
+    dev = torch.device("cuda:0")
+    samples = L * 320
+    fb = sidon.frontend.Fbank(dev)
+    gen = torch.Generator().manual_seed(9)
+    chunk = (torch.randn(B, samples, generator=gen) * 0.1).to(dev)
+    valid = torch.full((B,), samples, dtype=torch.int32, device=dev)
+    out = torch.empty(B, L, 160, device=dev)
+    ws = fb.workspace(B, samples)
+    graph = sidon.graphs.BucketGraphs().capture(("frontend", samples), lambda: fb(chunk, valid, out=out, workspace=ws))
+    stream = torch.cuda.current_stream()
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    steps = max(1, args.steps)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        graph.replay()
+    e1.record(stream)
+    e1.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    frames = samples // 160
+    return {
+        "metric": "ms per 96 s chunk (fbank front end, 1,536,000 samples -> [4800, 160])",
+        "value": ms, "unit": "ms", "n_gpus": 1, "steps": steps, "warmup": args.warmup,
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": FE_H100_MS / ms,
+        "vs_baseline_note": "speed-up over the reference's published GPU front end, 0.33 ms per chunk on H100 "
+                            "(README.md:42-43)",
+        "dtype": "fp32",
+        "data": "synthetic (16 kHz noise ~N(0, 0.1^2))",
+        "config": {"workload": "frontend: pad, framing GEMM [F,400]x[400,514] fp32, power + mel + log, per-bin "
+                               "normalization over the true frames, stacking", "batch": B, "samples": samples,
+                   "frames": frames},
+        "tflops": 2.0 * frames * 400 * 514 / (ms * 1e-3) / 1e12,
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -358,7 +403,7 @@ def main() -> int:
                     help="accepted for compatibility; parity is checked by tests/ (the oracle is used here only "
                          "for the CPU baseline)")
     ap.add_argument("--no-projections", action="store_true")
-    ap.add_argument("--workload", choices=["c3", "c4", "c5", "encoder"], default="c3")
+    ap.add_argument("--workload", choices=["c3", "c4", "c5", "encoder", "frontend"], default="c3")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run 3 plain device copies of 256 MiB (calibrates the HBM byte counters)")
     args = ap.parse_args()
@@ -388,6 +433,9 @@ def main() -> int:
         return 0
     if args.workload == "encoder":
         print(json.dumps(run_encoder(torch, sidon, args)), flush=True)
+        return 0
+    if args.workload == "frontend":
+        print(json.dumps(run_frontend(torch, sidon, args)), flush=True)
         return 0
     if args.workload == "c5":
         print(json.dumps(run_c5(torch, sidon, args)), flush=True)

@@ -8,6 +8,8 @@
 #ifndef SIDON_ENCODER_H
 #define SIDON_ENCODER_H
 
+#include <stddef.h>
+
 #include "sidon_flexrel.h"
 
 #ifdef __cplusplus
@@ -65,6 +67,50 @@ int sidon_silu(void* h, int64_t n, sidon_stream_t stream);
 int sidon_causal_dw_norm(const void* src, int glu_input, const float* dwt, const float* ln_w,
                          const float* ln_b, float eps, void* out, int B, int T, int C, int K,
                          sidon_stream_t stream);
+
+/*
+ * Fbank framing: frames[b, f, i] = chunk[b, 160 f + i - 160] (0 outside
+ * [0, S)) for f < F = S / 160, i < 400 -- the (160, 160) edge padding and the
+ * 400-sample frames with hop 160 of frontend.py:219-221, ready for the framing
+ * GEMM with the [400, 514] transform.  chunk [B, S] fp32 (S a positive
+ * multiple of 320), frames [B, F, 400] fp32, 16-byte aligned.
+ */
+int sidon_fbank_frames(const float* chunk, float* frames, int B, int S, sidon_stream_t stream);
+
+/*
+ * Fbank front end, after the framing GEMM.  Replaces the log-mel part of
+ * SeamlessFbank._masked, src/sidon_triton/frontend.py:218-229:
+ *
+ *   logmel[r, m] = log(max(sum_k mel[k, m] * (spec[r, k]^2 + spec[r, 257 + k]^2), 1.192092955078125e-07))
+ *
+ * spec [R, 514] fp32 (real 257 | imaginary 257 of each frame's 512-point
+ * rDFT, as the framing GEMM writes it), logmel [R, 80] fp32.  The mel bank
+ * is passed sparse: triangle m covers bins [mel_lo[m], mel_lo[m] + mel_len[m])
+ * with weights mel_w[m * max_len + i]; 1 <= max_len <= 257.
+ */
+int sidon_fbank_logmel(const float* spec, const float* mel_w, const int* mel_lo, const int* mel_len, int max_len,
+                       float* logmel, int R, sidon_stream_t stream);
+
+/* Bytes of the workspace sidon_fbank_normalize needs for B items of F frames. */
+size_t sidon_fbank_workspace_bytes(int B, int F);
+
+/*
+ * Per-bin normalization of B items of F frames (F even: a bucket of 160 F
+ * samples), replacing frontend.py:230-240.  valid [B] int32 on the device
+ * holds each item's true sample count; its true frames are
+ * tf = 1 + (valid + 320 - 400) / 160 (floor, clamped to [0, F]).  For every mel
+ * bin, over the frames f < tf:
+ *
+ *   feats[b, f, m] = (logmel[b, f, m] - mean) / sqrt(var + 1e-7)      (var with ddof 1)
+ *
+ * feats[b, tf, m] = 1.0 when tf is odd (the extractor's pad frame), and 0 for
+ * every later frame.  feats [B, F, 80] fp32 is also the stacked
+ * [B, F / 2, 160] encoder input.  workspace: device memory of at least
+ * sidon_fbank_workspace_bytes(B, F) bytes (overwritten); feats must not alias
+ * logmel.  tf = 1 gives 0/0 like the reference.
+ */
+int sidon_fbank_normalize(const float* logmel, const int* valid, float* workspace, size_t workspace_bytes,
+                          float* feats, int B, int F, sidon_stream_t stream);
 
 #ifdef __cplusplus
 }

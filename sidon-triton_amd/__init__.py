@@ -17,13 +17,15 @@ Entry points (same argument meaning as the reference):
     / ``encoder.load_encoder`` -- the whole 8-layer conformer encoder
     (triton_encoder.py:392-525);
   * ``runtime.EncoderRuntime`` -- bucketed, graph-captured encoder calls on
-    fixed max-size buffers (src/sidon_triton/runtime.py:74-186, :366-401).
+    fixed max-size buffers (src/sidon_triton/runtime.py:74-186, :366-401);
+  * ``frontend.Fbank`` -- the bucket-masked fbank front end that produces the
+    encoder's features and valid frames (src/sidon_triton/frontend.py:175-246).
 
 The package directory name is not a Python identifier; the repository's
 entry scripts load it under the module name ``sidon_triton_amd``.
 """
 
-from . import _lib, conformer, encoder, encoder_attention, encoder_block, flexrel, graphs, runtime
+from . import _lib, conformer, encoder, encoder_attention, encoder_block, flexrel, frontend, graphs, runtime
 from .flexrel import HEAD_DIM, LEFT, NUM_POS, RIGHT, flexrel_attention
 
 __all__ = [
@@ -37,6 +39,7 @@ __all__ = [
     "encoder_block",
     "flexrel",
     "flexrel_attention",
+    "frontend",
     "graphs",
     "runtime",
     "_lib",

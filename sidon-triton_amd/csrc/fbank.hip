@@ -1,0 +1,266 @@
+// fbank.hip -- the encoder's fbank front end around its framing GEMM
+// (MI355X / gfx950).  The framing GEMM (frames [R, 400] x the [400, 514]
+// DC-removal / pre-emphasis / window / rDFT matrix, fp32) runs in hipBLASLt;
+// these kernels do the rest of src/sidon_triton/frontend.py:218-240:
+//
+//   logmel     spec [R, 514] (re 257 | im 257) -> log(max(power . mel, 1.19e-7)) [R, 80]
+//   normalize  per (item, mel bin) over the item's true frames:
+//              (x - mean) / sqrt(var_ddof1 + 1e-7); the frame after an odd
+//              count of true frames is 1.0; later frames 0.  [B, F, 80] is
+//              also the stride-2 stacked [B, F / 2, 160] layout.
+//
+// logmel: one wavefront per frame; the 257 powers go to LDS, then lane m sums
+// the nonzero span of mel triangle m (sparse: start bin, length, weights).
+// normalize: statistics are per-tile two-pass sums (fixed tiles of frames,
+// one block per (tile, item)), merged in tile order by one block per item --
+// deterministic, no atomics -- through a caller-provided workspace; a third
+// kernel applies them to every frame.  frames: the edge padding and framing
+// that feed the framing GEMM.
+#include <hip/hip_runtime.h>
+
+#include <stdint.h>
+
+#include "sidon_encoder.h"
+#include "sidon_host.h"
+
+#define SIDON_API extern "C" __attribute__((visibility("default")))
+
+namespace {
+
+constexpr int kBins = 257;
+constexpr int kSpecWidth = 2 * kBins;
+constexpr int kMel = 80;
+constexpr int kFrameShift = 160;
+constexpr int kFrameSize = 400;
+constexpr int kEdgePad = 160;
+constexpr float kMelFloor = 1.192092955078125e-07f;
+constexpr float kVarEps = 1e-7f;
+constexpr float kPadValue = 1.0f;
+constexpr int kFramesPerBlock = 4;   // logmel: one wavefront each
+constexpr int kLanes = 4;            // normalize: frame lanes x 80 bins per block
+constexpr int kApplyFrames = 64;     // normalize: frames per apply block
+constexpr int kMaxTiles = 64;
+
+// frames[b, f, i] = chunk[b, 160 f + i - 160] (zero outside [0, S)): the
+// (160, 160) edge padding and the 400 / 160 framing in one pass, 4 samples
+// per thread.
+__global__ void __launch_bounds__(256) frames_kernel(const float* __restrict__ chunk, float* __restrict__ frames,
+                                                    int S, int F, int64_t total4) {
+  const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (q >= total4) return;
+  const int64_t e = q * 4;                       // element of [B, F, 400]
+  const int64_t row = e / kFrameSize;            // b * F + f
+  const int i = (int)(e - row * kFrameSize);     // 0, 4, ..., 396
+  const int64_t b = row / F;
+  const int f = (int)(row - b * F);
+  const int t0 = f * kFrameShift + i - kEdgePad;
+  const float* src = chunk + b * S;
+  float4 v;
+  v.x = (t0 >= 0 && t0 < S) ? src[t0] : 0.f;
+  v.y = (t0 + 1 >= 0 && t0 + 1 < S) ? src[t0 + 1] : 0.f;
+  v.z = (t0 + 2 >= 0 && t0 + 2 < S) ? src[t0 + 2] : 0.f;
+  v.w = (t0 + 3 >= 0 && t0 + 3 < S) ? src[t0 + 3] : 0.f;
+  *reinterpret_cast<float4*>(frames + e) = v;
+}
+
+__global__ void __launch_bounds__(64 * kFramesPerBlock) logmel_kernel(const float* __restrict__ spec,
+                                                                     const float* __restrict__ mel_w,
+                                                                     const int* __restrict__ mel_lo,
+                                                                     const int* __restrict__ mel_len, int max_len,
+                                                                     float* __restrict__ out, int R) {
+  __shared__ float power[kFramesPerBlock][kBins + 3];
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int r = blockIdx.x * kFramesPerBlock + w;
+  if (r < R) {
+    const float* row = spec + (int64_t)r * kSpecWidth;
+    for (int k = lane; k < kBins; k += 64) {
+      const float re = row[k];
+      const float im = row[kBins + k];
+      power[w][k] = re * re + im * im;
+    }
+  }
+  __syncthreads();
+  if (r >= R) return;
+  for (int m = lane; m < kMel; m += 64) {
+    const int lo = mel_lo[m];
+    const int n = mel_len[m];
+    const float* wm = mel_w + m * max_len;
+    float acc = 0.f;
+    for (int i = 0; i < n; ++i) acc = fmaf(wm[i], power[w][lo + i], acc);
+    out[(int64_t)r * kMel + m] = logf(fmaxf(acc, kMelFloor));
+  }
+}
+
+// True frames of the exact-length extractor for `samples` valid samples:
+// 1 + (samples + 2 * 160 - 400) / 160 (floor), clamped to [0, F].
+__device__ __forceinline__ int true_frames(int samples, int F) {
+  const int t = samples + 2 * kEdgePad - kFrameSize;
+  const int n = t < 0 ? 0 : t / kFrameShift + 1;
+  return min(n, F);
+}
+
+// Block (tile g, item b): two-pass sums over the true frames of tile g.
+__global__ void __launch_bounds__(kLanes * kMel) stats_kernel(const float* __restrict__ x,
+                                                             const int* __restrict__ valid,
+                                                             float* __restrict__ part, int F, int G) {
+  __shared__ float red[kLanes][kMel];
+  const int b = blockIdx.y;
+  const int g = blockIdx.x;
+  const int m = threadIdx.x % kMel;
+  const int fl = threadIdx.x / kMel;
+  const int tf = true_frames(valid[b], F);
+  const int per = (F + G - 1) / G;
+  const int f0 = g * per;
+  const int f1 = min(f0 + per, tf);
+  const int n = max(f1 - f0, 0);
+  const float* xb = x + (int64_t)b * F * kMel;
+  float s = 0.f;
+  for (int f = f0 + fl; f < f1; f += kLanes) s += xb[(int64_t)f * kMel + m];
+  red[fl][m] = s;
+  __syncthreads();
+  const float mean = n > 0 ? ((red[0][m] + red[1][m]) + (red[2][m] + red[3][m])) / (float)n : 0.f;
+  __syncthreads();
+  float q = 0.f;
+  for (int f = f0 + fl; f < f1; f += kLanes) {
+    const float d = xb[(int64_t)f * kMel + m] - mean;
+    q = fmaf(d, d, q);
+  }
+  red[fl][m] = q;
+  __syncthreads();
+  if (fl == 0) {
+    float* dst = part + (((int64_t)b * G + g) * kMel + m) * 3;
+    dst[0] = (float)n;
+    dst[1] = mean;
+    dst[2] = (red[0][m] + red[1][m]) + (red[2][m] + red[3][m]);
+  }
+}
+
+// Block b: merge item b's tile sums in tile order (Chan et al.'s pairwise
+// update of count, mean and sum of squared deviations) from LDS; writes
+// (mean, sqrt(var + eps)) per bin after the partials.
+__global__ void __launch_bounds__(256) merge_kernel(const int* __restrict__ valid, float* __restrict__ part, int F,
+                                                   int G, int B) {
+  __shared__ float sp[kMaxTiles * kMel * 3];
+  const int b = blockIdx.x;
+  const float* src = part + (int64_t)b * G * kMel * 3;
+  for (int i = threadIdx.x; i < G * kMel * 3; i += 256) sp[i] = src[i];
+  __syncthreads();
+  const int m = threadIdx.x;
+  if (m >= kMel) return;
+  const int tf = true_frames(valid[b], F);
+  float n = 0.f, mean = 0.f, m2 = 0.f;
+  for (int g = 0; g < G; ++g) {
+    const float* p = sp + (g * kMel + m) * 3;
+    const float nb = p[0];
+    if (nb <= 0.f) continue;
+    const float nt = n + nb;
+    const float d = p[1] - mean;
+    mean += d * (nb / nt);
+    m2 += p[2] + d * d * (n * nb / nt);
+    n = nt;
+  }
+  float* stats = part + (int64_t)B * G * kMel * 3 + ((int64_t)b * kMel + m) * 2;
+  stats[0] = mean;
+  stats[1] = sqrtf(m2 / (float)(tf - 1) + kVarEps);
+}
+
+// Block (frame range, item b): normalize the range's frames.
+__global__ void __launch_bounds__(kLanes * kMel) apply_kernel(const float* __restrict__ x,
+                                                             const int* __restrict__ valid,
+                                                             const float* __restrict__ part,
+                                                             float* __restrict__ out, int F, int G, int B) {
+  const int b = blockIdx.y;
+  const int m = threadIdx.x % kMel;
+  const int fl = threadIdx.x / kMel;
+  const int tf = true_frames(valid[b], F);
+  const float* stats = part + (int64_t)B * G * kMel * 3 + ((int64_t)b * kMel + m) * 2;
+  const float mean = stats[0];
+  const float denom = stats[1];
+  const float* xb = x + (int64_t)b * F * kMel;
+  float* ob = out + (int64_t)b * F * kMel;
+  const int fbase = blockIdx.x * kApplyFrames;
+  for (int i = fl; i < kApplyFrames; i += kLanes) {
+    const int f = fbase + i;
+    if (f >= F) break;
+    float v;
+    if (f < tf) {
+      v = (xb[(int64_t)f * kMel + m] - mean) / denom;
+    } else {
+      v = (f == tf && (tf & 1)) ? kPadValue : 0.f;
+    }
+    ob[(int64_t)f * kMel + m] = v;
+  }
+}
+
+int tiles_for(int F) { return F / 128 < 1 ? 1 : (F / 128 > kMaxTiles ? kMaxTiles : F / 128); }
+
+}  // namespace
+
+SIDON_API int sidon_fbank_logmel(const float* spec, const float* mel_w, const int* mel_lo, const int* mel_len,
+                                 int max_len, float* logmel, int R, sidon_stream_t stream) {
+  using sidon::fail;
+  sidon::clear_error();
+  if (!spec || !mel_w || !mel_lo || !mel_len || !logmel) return fail(SIDON_E_NULL, "every pointer must be non-NULL");
+  if (R < 1 || max_len < 1 || max_len > kBins) return fail(SIDON_E_SHAPE, "R=%d must be >= 1 and max_len=%d in [1, %d]", R, max_len, kBins);
+  int rc;
+  if ((rc = sidon::check_device())) return rc;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(logmel_kernel, dim3((unsigned)((R + kFramesPerBlock - 1) / kFramesPerBlock)),
+                     dim3(64 * kFramesPerBlock), 0, s, spec, mel_w, mel_lo, mel_len, max_len, logmel, R);
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return fail(SIDON_E_LAUNCH, "fbank logmel launch failed: %s", hipGetErrorString(err));
+  return SIDON_OK;
+}
+
+SIDON_API int sidon_fbank_frames(const float* chunk, float* frames, int B, int S, sidon_stream_t stream) {
+  using sidon::fail;
+  sidon::clear_error();
+  if (!chunk || !frames) return fail(SIDON_E_NULL, "chunk and frames must be non-NULL");
+  if (B < 1 || S < 2 * kFrameShift || S % (2 * kFrameShift) != 0)
+    return fail(SIDON_E_SHAPE, "B=%d must be >= 1 and S=%d a positive multiple of %d", B, S, 2 * kFrameShift);
+  if (!sidon::aligned16(frames)) return fail(SIDON_E_ALIGN, "frames must be 16-byte aligned");
+  int rc;
+  if ((rc = sidon::check_device())) return rc;
+  const int F = S / kFrameShift;
+  const int64_t total4 = (int64_t)B * F * kFrameSize / 4;
+  hipLaunchKernelGGL(frames_kernel, dim3((unsigned)((total4 + 255) / 256)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), chunk, frames, S, F, total4);
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return fail(SIDON_E_LAUNCH, "fbank frames launch failed: %s", hipGetErrorString(err));
+  return SIDON_OK;
+}
+
+SIDON_API size_t sidon_fbank_workspace_bytes(int B, int F) {
+  if (B < 1 || F < 1) return 0;
+  return (size_t)B * (tiles_for(F) * kMel * 3 + kMel * 2) * sizeof(float);
+}
+
+SIDON_API int sidon_fbank_normalize(const float* logmel, const int* valid, float* workspace, size_t workspace_bytes,
+                                    float* feats, int B, int F, sidon_stream_t stream) {
+  using sidon::fail;
+  sidon::clear_error();
+  if (!logmel || !valid || !workspace || !feats) return fail(SIDON_E_NULL, "every pointer must be non-NULL");
+  if (B < 1 || F < 2 || (F & 1) != 0) return fail(SIDON_E_SHAPE, "B=%d must be >= 1 and F=%d even and >= 2", B, F);
+  if (workspace_bytes < sidon_fbank_workspace_bytes(B, F))
+    return fail(SIDON_E_SHAPE, "workspace of %zu bytes is smaller than the %zu needed", workspace_bytes,
+                sidon_fbank_workspace_bytes(B, F));
+  if (logmel == feats) return fail(SIDON_E_SHAPE, "feats must not alias logmel");
+  int rc;
+  if ((rc = sidon::check_device())) return rc;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int G = tiles_for(F);
+  hipLaunchKernelGGL(stats_kernel, dim3(G, B), dim3(kLanes * kMel), 0, s, logmel, valid, workspace, F, G);
+  hipError_t err = hipGetLastError();
+  if (err == hipSuccess) {
+    hipLaunchKernelGGL(merge_kernel, dim3(B), dim3(256), 0, s, valid, workspace, F, G, B);
+    err = hipGetLastError();
+  }
+  if (err == hipSuccess) {
+    hipLaunchKernelGGL(apply_kernel, dim3((F + kApplyFrames - 1) / kApplyFrames, B), dim3(kLanes * kMel), 0, s,
+                       logmel, valid, workspace, feats, F, G, B);
+    err = hipGetLastError();
+  }
+  if (err != hipSuccess) return fail(SIDON_E_LAUNCH, "fbank normalize launch failed: %s", hipGetErrorString(err));
+  return SIDON_OK;
+}

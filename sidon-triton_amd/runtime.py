@@ -14,10 +14,14 @@ Mirrors the encoder side of src/sidon_triton/runtime.py:
     past ``max_graphs`` (:374-401, via ``graphs.BucketGraphs``);
   * all work enqueued on a non-default compute stream (:27, :360).
 
-The valid rows of a bucketed run equal an exact-length run: the attention
-masks the padded keys, the depthwise conv is causal and every other op is
-row-wise.  The waveform front end and the decoder are not part of this
-runtime: it takes the 160-channel features.
+The valid rows of a bucketed run equal an exact-length run: the front end
+takes its statistics over the true frames only, the attention masks the
+padded keys, the depthwise conv is causal and every other op is row-wise.
+
+Two entries: ``run`` takes 160-channel features (bucketed in frames);
+``run_wave`` takes 16 kHz waveforms and runs the fbank front end and the
+encoder in one graph per (batch, bucket), bucketed in samples exactly as
+runtime.py:366-372 does.  The decoder is not part of this runtime.
 """
 
 from __future__ import annotations
@@ -25,12 +29,17 @@ from __future__ import annotations
 import torch
 
 from .encoder import HipEncoder
+from .frontend import BUCKET_QUANTUM, Fbank, num_features
 from .graphs import BucketGraphs
 
 FRAME_RATE = 50                 # encoder frames per second
 FINE_BUCKET_FRAMES = 50         # 1 s
 FINE_LIMIT_FRAMES = 32 * 50     # 32 s
 COARSE_BUCKET_FRAMES = 4 * 50   # 4 s
+IN_RATE = 16_000
+FINE_BUCKET_SAMPLES = IN_RATE           # 1 s
+FINE_LIMIT_SAMPLES = 32 * IN_RATE       # 32 s
+COARSE_BUCKET_SAMPLES = 4 * IN_RATE     # 4 s
 MIN_SEQ = 2
 
 
@@ -42,11 +51,20 @@ def bucket_frames(frames: int, max_frames: int) -> int:
     return min(max_frames, -(-frames // step) * step)
 
 
+def bucket_samples(samples: int, max_samples: int) -> int:
+    """Bucket length (samples, a multiple of 320) of a chunk of ``samples``
+    samples (runtime.py:366-372)."""
+    if samples < 1:
+        raise ValueError("a chunk needs at least one sample")
+    step = FINE_BUCKET_SAMPLES if samples <= FINE_LIMIT_SAMPLES else COARSE_BUCKET_SAMPLES
+    return min(max_samples, -(-samples // step) * step)
+
+
 class EncoderRuntime:
     """Encoder calls on bucketed, graph-captured, fixed-address buffers."""
 
     def __init__(self, encoder: HipEncoder, max_batch: int = 1, max_seconds: float = 96.0,
-                 use_graph: bool = True, max_graphs: int = 48) -> None:
+                 use_graph: bool = True, max_graphs: int = 48, frontend: Fbank | None = None) -> None:
         self.encoder = encoder
         self.max_batch = int(max_batch)
         self.max_seq = int(max_seconds * FRAME_RATE)
@@ -61,6 +79,12 @@ class EncoderRuntime:
         self.use_graph = use_graph
         self.graphs = BucketGraphs(max_graphs)
         self.compute = torch.cuda.Stream(device=device)
+        self.frontend = frontend
+        self.max_samples = self.max_seq * BUCKET_QUANTUM
+        if frontend is not None:
+            self.wave = torch.zeros(b * self.max_samples, device=device)
+            self.wave_valid = torch.zeros(b, dtype=torch.int32, device=device)
+            self.fbank_workspace = frontend.workspace(b, self.max_samples)
 
     def bucket(self, frames: int) -> int:
         return bucket_frames(frames, self.max_seq)
@@ -105,3 +129,44 @@ class EncoderRuntime:
                 self._enqueue(batch, length)
         caller.wait_stream(self.compute)
         return hidden[:, :n]
+
+    def _enqueue_wave(self, batch: int, samples: int) -> None:
+        length = samples // BUCKET_QUANTUM
+        feats, hidden = self._views(batch, length)
+        wave = self.wave[:batch * samples].view(batch, samples)
+        self.frontend(wave, self.wave_valid[:batch], out=feats, workspace=self.fbank_workspace)
+        self.encoder(feats, self.lens[:batch], out=hidden, workspace=self.workspace)
+
+    def run_wave(self, wave: torch.Tensor, samples=None) -> torch.Tensor:
+        """wave [B, n] 16 kHz fp32 (any device) with ``samples`` true samples
+        per item (None: all n) -> hidden [B, num_features(n), C], a view of the
+        runtime's buffer valid until the next call; item b's first
+        num_features(samples[b]) rows are its valid frames.  Front end and
+        encoder run as one graph per (batch, bucket)."""
+        if self.frontend is None:
+            raise RuntimeError("this runtime was built without a front end")
+        batch, n = wave.shape
+        if not 1 <= batch <= self.max_batch:
+            raise ValueError(f"batch {batch} outside [1, {self.max_batch}]")
+        samples = [n] * batch if samples is None else [int(x) for x in samples]
+        if len(samples) != batch or max(samples) > n or min(num_features(x) for x in samples) < MIN_SEQ:
+            raise ValueError(f"samples {samples} must lie in [1, {n}] and give >= {MIN_SEQ} frames")
+        if n > self.max_samples:
+            raise ValueError(f"{n} samples exceed the runtime's maximum of {self.max_samples}")
+        bucket = bucket_samples(n, self.max_samples)
+        caller = torch.cuda.current_stream(self.encoder.device)
+        self.compute.wait_stream(caller)
+        with torch.cuda.stream(self.compute):
+            view = self.wave[:batch * bucket].view(batch, bucket)
+            view[:, :n].copy_(wave, non_blocking=True)
+            for b, x in enumerate(samples):
+                view[b, x:].zero_()
+            self.wave_valid[:batch].copy_(torch.tensor(samples, dtype=torch.int32))
+            self.lens[:batch].copy_(torch.tensor([num_features(x) for x in samples], dtype=torch.int32))
+            if self.use_graph:
+                self.graphs.run(("wave", batch, bucket), lambda: self._enqueue_wave(batch, bucket))
+            else:
+                self._enqueue_wave(batch, bucket)
+        caller.wait_stream(self.compute)
+        _, hidden = self._views(batch, bucket // BUCKET_QUANTUM)
+        return hidden[:, :num_features(n)]
