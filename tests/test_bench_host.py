@@ -25,3 +25,24 @@ def test_c4_clips_follow_the_reference_draws():
 def test_attention_flops_at_c3():
     # 4 B H L^2 D + 2 B H L 73 D at L=4800: 95.09 GFLOP per layer
     assert math.isclose(bench.attention_flops(16, 4800, 4800), 95.09e9, rel_tol=1e-3)
+
+
+def test_encoder_flops_at_96s():
+    # per layer: FFN 2 x (2 x 1024 x 4096), QKV 3 x 1024^2, out 1024^2, pointwise
+    # convs 2 x 1024^2 + 1024^2 (multiply-adds), plus the feature projection, the
+    # depthwise conv and the attention: 2617 GFLOP per 96 s chunk
+    gemm = 2.0 * 4800 * (160 * 1024 + 8 * (4 * 1024 * 4096 + 4 * 1024 * 1024 + 3 * 1024 * 1024))
+    conv = 8 * 2.0 * 4800 * 1024 * 31
+    attn = 8 * bench.attention_flops(16, 4800, 4800)
+    assert math.isclose(bench.encoder_flops(4800), gemm + conv + attn, rel_tol=1e-12)
+    assert math.isclose(bench.encoder_flops(4800), 2617e9, rel_tol=1e-3)
+
+
+def test_encoder_model_weights_shapes():
+    import torch
+
+    w = bench.encoder_model_weights(torch, layers=1)
+    p = w["layers"][0]
+    assert w["heads"] == 16 and w["fp_w"].shape == (1024, 160)
+    assert p["ffn1_w1"].shape == (4096, 1024) and p["ffn2_w2"].shape == (1024, 4096)
+    assert p["pw1_w"].shape == (2048, 1024) and p["dw_w"].shape == (1024, 31) and p["rel"].shape == (73, 64)
