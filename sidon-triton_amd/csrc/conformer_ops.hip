@@ -66,19 +66,33 @@ __device__ __forceinline__ _Float16 silu1(float x) {
 
 // ---- glu / silu -------------------------------------------------------------
 
-// 8 columns per thread; requires C % 8 == 0 and 16-byte aligned rows.
+// kVec chunks of 8 columns per thread (loads first, then math); requires
+// C % 8 == 0 and 16-byte aligned rows.
+constexpr int kVec = 4;
 __global__ void __launch_bounds__(kEwThreads) glu_vec_kernel(const _Float16* __restrict__ h, _Float16* __restrict__ g,
                                                              int64_t n8, int c8) {
-  const int64_t i = (int64_t)blockIdx.x * kEwThreads + threadIdx.x;
-  if (i >= n8) return;
-  const int64_t row = i / c8;
-  const int64_t col = i - row * c8;
-  const h8 a = reinterpret_cast<const h8*>(h)[row * 2 * c8 + col];
-  const h8 b = reinterpret_cast<const h8*>(h)[row * 2 * c8 + c8 + col];
-  h8 o;
+  const int64_t i0 = ((int64_t)blockIdx.x * kEwThreads * kVec) + threadIdx.x;
+  h8 a[kVec], b[kVec];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) o[j] = glu1((float)a[j], (float)b[j]);
-  reinterpret_cast<h8*>(g)[i] = o;
+  for (int v = 0; v < kVec; ++v) {
+    const int64_t i = i0 + (int64_t)v * kEwThreads;
+    if (i < n8) {
+      const int64_t row = i / c8;
+      const int64_t col = i - row * c8;
+      a[v] = reinterpret_cast<const h8*>(h)[row * 2 * c8 + col];
+      b[v] = reinterpret_cast<const h8*>(h)[row * 2 * c8 + c8 + col];
+    }
+  }
+#pragma unroll
+  for (int v = 0; v < kVec; ++v) {
+    const int64_t i = i0 + (int64_t)v * kEwThreads;
+    if (i < n8) {
+      h8 o;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[j] = glu1((float)a[v][j], (float)b[v][j]);
+      reinterpret_cast<h8*>(g)[i] = o;
+    }
+  }
 }
 
 __global__ void __launch_bounds__(kEwThreads) glu_scalar_kernel(const _Float16* __restrict__ h,
@@ -93,14 +107,22 @@ __global__ void __launch_bounds__(kEwThreads) glu_scalar_kernel(const _Float16* 
 }
 
 __global__ void __launch_bounds__(kEwThreads) silu_vec_kernel(_Float16* __restrict__ h, int64_t n8) {
-  const int64_t i = (int64_t)blockIdx.x * kEwThreads + threadIdx.x;
-  if (i >= n8) return;
-  h8 v = reinterpret_cast<h8*>(h)[i];
+  const int64_t i0 = ((int64_t)blockIdx.x * kEwThreads * kVec) + threadIdx.x;
+  h8 x[kVec];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    v[j] = silu1((float)v[j]);
+  for (int v = 0; v < kVec; ++v) {
+    const int64_t i = i0 + (int64_t)v * kEwThreads;
+    if (i < n8) x[v] = reinterpret_cast<const h8*>(h)[i];
   }
-  reinterpret_cast<h8*>(h)[i] = v;
+#pragma unroll
+  for (int v = 0; v < kVec; ++v) {
+    const int64_t i = i0 + (int64_t)v * kEwThreads;
+    if (i < n8) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) x[v][j] = silu1((float)x[v][j]);
+      reinterpret_cast<h8*>(h)[i] = x[v];
+    }
+  }
 }
 
 __global__ void __launch_bounds__(kEwThreads) silu_scalar_kernel(_Float16* __restrict__ h, int64_t n) {
@@ -363,7 +385,8 @@ SIDON_API int sidon_glu(const void* h, void* g, int R, int C, sidon_stream_t str
   auto* gp = static_cast<_Float16*>(g);
   if (C % 8 == 0 && aligned(h, 16) && aligned(g, 16)) {
     const int64_t n8 = (int64_t)R * (C / 8);
-    hipLaunchKernelGGL(glu_vec_kernel, dim3((unsigned)((n8 + kEwThreads - 1) / kEwThreads)), dim3(kEwThreads), 0, s, hp,
+    const int64_t per_block = (int64_t)kEwThreads * kVec;
+    hipLaunchKernelGGL(glu_vec_kernel, dim3((unsigned)((n8 + per_block - 1) / per_block)), dim3(kEwThreads), 0, s, hp,
                        gp, n8, C / 8);
   } else {
     const int64_t n = (int64_t)R * C;
@@ -387,7 +410,8 @@ SIDON_API int sidon_silu(void* h, int64_t n, sidon_stream_t stream) {
   auto* hp = static_cast<_Float16*>(h);
   if (n % 8 == 0 && aligned(h, 16)) {
     const int64_t n8 = n / 8;
-    hipLaunchKernelGGL(silu_vec_kernel, dim3((unsigned)((n8 + kEwThreads - 1) / kEwThreads)), dim3(kEwThreads), 0, s, hp,
+    const int64_t per_block = (int64_t)kEwThreads * kVec;
+    hipLaunchKernelGGL(silu_vec_kernel, dim3((unsigned)((n8 + per_block - 1) / per_block)), dim3(kEwThreads), 0, s, hp,
                        n8);
   } else {
     hipLaunchKernelGGL(silu_scalar_kernel, dim3((unsigned)((n + kEwThreads - 1) / kEwThreads)), dim3(kEwThreads), 0, s,

@@ -116,12 +116,14 @@ __global__ void __launch_bounds__(kLanes * kMel) stats_kernel(const float* __res
   const int n = max(f1 - f0, 0);
   const float* xb = x + (int64_t)b * F * kMel;
   float s = 0.f;
+#pragma unroll 8
   for (int f = f0 + fl; f < f1; f += kLanes) s += xb[(int64_t)f * kMel + m];
   red[fl][m] = s;
   __syncthreads();
   const float mean = n > 0 ? ((red[0][m] + red[1][m]) + (red[2][m] + red[3][m])) / (float)n : 0.f;
   __syncthreads();
   float q = 0.f;
+#pragma unroll 8
   for (int f = f0 + fl; f < f1; f += kLanes) {
     const float d = xb[(int64_t)f * kMel + m] - mean;
     q = fmaf(d, d, q);
@@ -144,6 +146,7 @@ __global__ void __launch_bounds__(256) merge_kernel(const int* __restrict__ vali
   __shared__ float sp[kMaxTiles * kMel * 3];
   const int b = blockIdx.x;
   const float* src = part + (int64_t)b * G * kMel * 3;
+#pragma unroll 8
   for (int i = threadIdx.x; i < G * kMel * 3; i += 256) sp[i] = src[i];
   __syncthreads();
   const int m = threadIdx.x;

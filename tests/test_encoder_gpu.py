@@ -123,7 +123,7 @@ def test_encoder_matches_transformers_golden(sidon, name):
     for b, n in enumerate(lens):
         err = errors(expected[b, :n], got[b, :n])
         print(name, b, err)
-        assert err["snr_db"] > 45 and err["max_abs"] < 0.05, (b, err)
+        assert err["snr_db"] > 65 and err["max_abs"] < 5e-3, (b, err)  # measured 69.4-69.7 dB, 1.5e-3
 
 
 @pytest.fixture(scope="module")
@@ -144,7 +144,8 @@ def test_full_width_encoder_matches_fp32_oracle(sidon, full_width, length, valid
     err = errors(want[0, :valid].double().cpu().numpy(), got[0, :valid].double().cpu().numpy())
     print(length, valid, err)
     assert torch.isfinite(got).all()
-    assert err["snr_db"] > 45 and err["max_abs"] < 0.05 * want.abs().max().item(), err
+    # measured 62.2-62.3 dB, max |err| 5e-3 (the reference reports 66.6-67.1 dB with real weights)
+    assert err["snr_db"] > 58 and err["max_abs"] < 0.02 * want.abs().max().item(), err
 
 
 def test_bucketed_run_matches_exact_length_run(sidon, full_width):
