@@ -12,7 +12,9 @@ Mirrors src/sidon_triton/triton_encoder.py:
     residual stream kept in fp32 and every residual GEMM accumulating into it
     (fp16 operands, fp32 output), the norms fused with the bias adds;
   * ``save_encoder`` / ``load_encoder`` (:514-525): here a safetensors file
-    with the scalars in its metadata, loaded without unpickling anything.
+    with the scalars in its metadata, loaded without unpickling anything;
+    ``load_encoder`` also reads the reference's own ``encoder_triton.pt``
+    (with ``torch.load(weights_only=True)``).
 
 Per layer the work is: res_norm (HIP), hipBLASLt GEMMs through torch, SiLU
 (HIP, in place), the relative_key attention (HIP), and the conv module's
@@ -277,7 +279,32 @@ def read_encoder(path) -> tuple[dict, int, float]:
     return packed, int(meta["max_batch"]), float(meta["max_seconds"])
 
 
+def read_triton_encoder(path) -> tuple[dict, int, float]:
+    """Read the reference's own packed file (``encoder_triton.pt`` of
+    ``save_encoder``, src/sidon_triton/triton_encoder.py:514-518): a dict of
+    tensors, tuples and numbers, so it loads with ``weights_only=True`` (the
+    reference's loader, :521-525, unpickles arbitrary objects; this one does
+    not).  The packed layout is the one ``pack_weights`` writes, key for key.
+    -> (packed weights on the CPU, max_batch, max_seconds)."""
+    saved = torch.load(str(Path(path)), map_location="cpu", weights_only=True)
+    if not isinstance(saved, dict) or "packed" not in saved:
+        raise ValueError(f"{path} is not a packed encoder file")
+    packed = saved["packed"]
+    missing = {"heads", "fp_ln", "fp_w", "fp_b", "layers"} - set(packed)
+    if missing:
+        raise ValueError(f"{path}: packed weights lack {sorted(missing)}")
+    layer_keys = set(_NORMS) | set(_LAYER_TENSORS) | {"cum_bias"}
+    for i, layer in enumerate(packed["layers"]):
+        if set(layer) != layer_keys:
+            raise ValueError(f"{path}: layer {i} keys differ from the packed layout")
+    return packed, int(saved["max_batch"]), float(saved["max_seconds"])
+
+
 def load_encoder(path, device="cuda") -> tuple[HipEncoder, int, float]:
-    """-> (HipEncoder, max_batch, max_seconds)."""
-    packed, max_batch, max_seconds = read_encoder(path)
+    """-> (HipEncoder, max_batch, max_seconds) from this library's
+    safetensors file or from the reference's ``encoder_triton.pt``."""
+    path = Path(path)
+    with open(path, "rb") as f:
+        zip_magic = f.read(2) == b"PK"   # torch.save writes a zip archive
+    packed, max_batch, max_seconds = read_triton_encoder(path) if zip_magic else read_encoder(path)
     return HipEncoder(packed, device), max_batch, max_seconds

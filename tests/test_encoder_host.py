@@ -111,3 +111,44 @@ def test_bucket_cap(pkg):
     assert pkg.runtime.bucket_frames(4700, 4750) == 4750
     with pytest.raises(ValueError):
         pkg.runtime.bucket_frames(0, 4800)
+
+
+def test_reads_the_reference_packed_file(pkg, tmp_path):
+    # The reference's save_encoder writes {"packed": ..., "max_batch": ...,
+    # "max_seconds": ...} with torch.save (src/sidon_triton/triton_encoder.py:514-518);
+    # the packed layout is key for key the one pack_weights writes.
+    packed = pkg.encoder.pack_weights(encoder_weights(2, 2, seed=6))
+    path = tmp_path / "encoder_triton.pt"
+    torch.save({"packed": packed, "max_batch": 1, "max_seconds": 96.0}, str(path))
+    got, max_batch, max_seconds = pkg.encoder.read_triton_encoder(path)
+    assert (max_batch, max_seconds) == (1, 96.0)
+    for g, p in zip(got["layers"], packed["layers"]):
+        for key, val in p.items():
+            if key == "cum_bias":
+                assert all(_eq(a, b) for a, b in zip(g[key], val))
+            elif isinstance(val, tuple):
+                assert _eq(g[key][0], val[0]) and g[key][2] == val[2]
+            else:
+                assert _eq(g[key], val), key
+
+
+def test_reference_file_with_other_layout_is_rejected(pkg, tmp_path):
+    packed = pkg.encoder.pack_weights(encoder_weights(2, 1, seed=6))
+    del packed["layers"][0]["rel"]
+    path = tmp_path / "bad.pt"
+    torch.save({"packed": packed, "max_batch": 1, "max_seconds": 96.0}, str(path))
+    with pytest.raises(ValueError):
+        pkg.encoder.read_triton_encoder(path)
+
+
+def test_load_encoder_reads_both_formats(pkg, tmp_path):
+    packed = pkg.encoder.pack_weights(encoder_weights(2, 2, seed=7))
+    ours = tmp_path / "enc.safetensors"
+    theirs = tmp_path / "encoder_triton.pt"
+    pkg.encoder.save_encoder(packed, max_batch=2, max_seconds=40.0, path=ours)
+    torch.save({"packed": packed, "max_batch": 3, "max_seconds": 96.0}, str(theirs))
+    a, ba, sa = pkg.encoder.load_encoder(ours, device="cpu")
+    b, bb, sb = pkg.encoder.load_encoder(theirs, device="cpu")
+    assert (ba, sa, bb, sb) == (2, 40.0, 3, 96.0)
+    assert a.heads == b.heads == 2 and a.hidden == b.hidden == 128 and a.inter == b.inter == 256
+    assert _eq(a.layers[1]["qkv_w"], b.layers[1]["qkv_w"])
