@@ -19,13 +19,17 @@ Entry points (same argument meaning as the reference):
   * ``runtime.EncoderRuntime`` -- bucketed, graph-captured encoder calls on
     fixed max-size buffers (src/sidon_triton/runtime.py:74-186, :366-401);
   * ``frontend.Fbank`` -- the bucket-masked fbank front end that produces the
-    encoder's features and valid frames (src/sidon_triton/frontend.py:175-246).
+    encoder's features and valid frames (src/sidon_triton/frontend.py:175-246);
+  * ``modeling.HipRelSelfAttention`` / ``modeling.replace_attention_with_hip``
+    -- the module drop-in for transformers' relative_key self-attention
+    (src/sidon_triton/modeling.py:40-131).
 
 The package directory name is not a Python identifier; the repository's
 entry scripts load it under the module name ``sidon_triton_amd``.
 """
 
-from . import _lib, conformer, encoder, encoder_attention, encoder_block, flexrel, frontend, graphs, runtime
+from . import (_lib, conformer, encoder, encoder_attention, encoder_block, flexrel, frontend, graphs, modeling,
+               runtime)
 from .flexrel import HEAD_DIM, LEFT, NUM_POS, RIGHT, flexrel_attention
 
 __all__ = [
@@ -41,6 +45,7 @@ __all__ = [
     "flexrel_attention",
     "frontend",
     "graphs",
+    "modeling",
     "runtime",
     "_lib",
 ]
