@@ -384,11 +384,18 @@ flexrel_fwd_kernel(const Params p) {
   const int kperm = mfma_row_perm(n);
   const char* krow0 = ring + kperm * 128;
   const int kswz = tile_swz(kperm);
+  // The swizzled chunk offsets differ per lane and per k-step, so the eight
+  // addresses (two slots x four k-steps) are formed once, not per step.
+  const char* kaddr[2][4];
+#pragma unroll
+  for (int sl = 0; sl < 2; ++sl)
+#pragma unroll
+    for (int s = 0; s < 4; ++s) kaddr[sl][s] = krow0 + sl * kTile + (((2 * s + g) ^ kswz) << 4);
   auto load_k = [&](uint32_t slot) SIDON_INLINE {
-    const char* krow = krow0 + slot;
+    const int sl = slot != 0;
 #pragma unroll
     for (int s = 0; s < 4; ++s)
-      kop[s] = *reinterpret_cast<const h8*>(krow + (((2 * s + g) ^ kswz) << 4));
+      kop[s] = *reinterpret_cast<const h8*>(sl ? kaddr[1][s] : kaddr[0][s]);
   };
   // V^T operands via transpose reads: group G of 16 lanes, source lane
   // (a, bq) reads V[key0 + a][d0 + 4 bq .. +4) with key0 = 16 hh + 8 (G / 2)
@@ -444,10 +451,14 @@ flexrel_fwd_kernel(const Params p) {
   // non-finite probability of one query never reaches another's sum.  One
   // accumulator serves both column blocks: block 0's sums are read at the
   // start of the half step that issues block 1's.
-  const h8 ones = {1, 1, 1, 1, 1, 1, 1, 1};
+  // Kept live in registers across the loop (otherwise it is rebuilt with two
+  // 64-bit moves before every row-sum pair).
+  h8 ones = {1, 1, 1, 1, 1, 1, 1, 1};
+  asm volatile("" : "+v"(ones));
   f32x16 rs;
   float l_run[2] = {0.f, 0.f};
   auto rowsum = [&](int qb) SIDON_INLINE {
+    asm volatile("" : "+v"(ones));
     rs = __builtin_amdgcn_mfma_f32_32x32x16_f16(ones, pk[qb][0], f32x16{}, 0, 0, 0);
     rs = __builtin_amdgcn_mfma_f32_32x32x16_f16(ones, pk[qb][1], rs, 0, 0, 0);
   };
