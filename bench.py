@@ -409,7 +409,8 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py runs on one GPU only: this build has no multi-GPU path "
-              "(each 96 s chunk is independent; see DESIGN.md for how it would shard)", file=sys.stderr)
+              "(each 96 s chunk is independent, so the natural scale-out is one process per GPU over "
+              "chunks, with no collectives)", file=sys.stderr)
         return 2
 
     import torch
