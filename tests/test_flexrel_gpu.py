@@ -197,3 +197,49 @@ def test_lens_clamped_to_length(sidon):
     a = run(sidon, q, k, v, rel, [90])
     b = run(sidon, q, k, v, rel, [100000])
     assert torch.equal(a, b)
+
+
+def test_batch_with_mixed_valid_lengths_L1500(sidon):
+    """B=4 items of one bucket with very different valid lengths (full, c2's 1463,
+    about half, one key): every item against the oracle on its own length."""
+    B, H, L = 4, 8, 1500
+    lens = [1500, 1463, 777, 1]
+    q, k, v, rel = seeded_inputs(B, H, L, seed=91)
+    got = run(sidon, q, k, v, rel, lens).float().cpu().numpy()
+    heads = [0, 7]
+    ref = flexrel_reference(q.numpy()[:, heads], k.numpy()[:, heads], v.numpy()[:, heads], rel.numpy(), lens)
+    assert_parity(ref, got[:, heads], lens, "mixed-lens")
+    assert np.isfinite(got).all()
+
+
+def test_six_items_short_bucket(sidon):
+    """B=6 at L=512: lengths on and around the 32-key step and 64-row block edges."""
+    B, H, L = 6, 4, 512
+    lens = [512, 511, 257, 256, 33, 1]
+    q, k, v, rel = seeded_inputs(B, H, L, seed=92)
+    got = run(sidon, q, k, v, rel, lens).float().cpu().numpy()
+    ref = flexrel_reference(q.numpy(), k.numpy(), v.numpy(), rel.numpy(), lens)
+    assert_parity(ref, got, lens, "six-items")
+
+
+@pytest.mark.parametrize("H", [1, 5, 32])
+def test_other_head_counts(sidon, H):
+    """Head counts other than the encoder's 16 (grid and XCD mapping follow B*H)."""
+    B, L = 1, 640
+    q, k, v, rel = seeded_inputs(B, H, L, seed=93 + H)
+    got = run(sidon, q, k, v, rel, [601]).float().cpu().numpy()
+    heads = sorted({0, H // 2, H - 1})
+    ref = flexrel_reference(q.numpy()[:, heads], k.numpy()[:, heads], v.numpy()[:, heads], rel.numpy(), [601])
+    assert_parity(ref, got[:, heads], [601], f"H={H}")
+
+
+def test_long_sequence_L9600(sidon):
+    """Twice the c3 length (192 s of frames, 2400 workgroups): two heads against
+    the oracle, every row finite."""
+    B, H, L = 1, 16, 9600
+    q, k, v, rel = seeded_inputs(B, H, L, seed=94)
+    got = run(sidon, q, k, v, rel).float().cpu().numpy()
+    assert np.isfinite(got).all()
+    heads = [2, 13]
+    ref = flexrel_reference(q.numpy()[:, heads], k.numpy()[:, heads], v.numpy()[:, heads], rel.numpy())
+    assert_parity(ref, got[:, heads], [L], "L=9600")
