@@ -50,6 +50,29 @@ int sidon_glu(const void* h, void* g, int R, int C, sidon_stream_t stream);
 int sidon_silu(void* h, int64_t n, sidon_stream_t stream);
 
 /*
+ * The feed-forward module's input projection with its bias and SiLU fused:
+ *
+ *   y[m, n] = act(fp16(x[m, :] . w[n, :] + bias[n]))     act: 1 = SiLU, 0 = none
+ *
+ * x [M, K] and w [N, K] fp16 (row strides ldx, ldw; both K-contiguous),
+ * fp32 sums, y [M, N] fp16 (row stride ldy); bias fp16 [N] or NULL.  SiLU
+ * is taken in fp32 on the fp16-rounded sum and rounded to fp16, as
+ * sidon_silu does after a separate GEMM.  Replaces the torch.addmm(b1, xn,
+ * W1^T) + in-place F.silu pair of src/sidon_triton/triton_encoder.py:485-486
+ * and :505-506.  Shapes: M >= 1, N a multiple of 256, K a multiple of 64;
+ * strides multiples of 8; x, w, y 16-byte aligned, bias 8-byte aligned.
+ * sidon_gemm_bias_act_fits(M, N, K) says whether a shape is supported (pure
+ * host function); sidon_gemm_bias_act_preferred(M, N, K) whether the kernel
+ * is expected to beat a library GEMM followed by sidon_silu on the current
+ * device (its 320 x 256 tiles keep >= 3/4 of the CUs busy in every round).
+ * Neither has a counterpart in the reference.
+ */
+int sidon_gemm_bias_act_fits(int M, int N, int K);
+int sidon_gemm_bias_act_preferred(int M, int N, int K);
+int sidon_gemm_bias_act(const void* x, int ldx, const void* w, int ldw, const void* bias, void* y, int ldy,
+                        int M, int N, int K, int act, sidon_stream_t stream);
+
+/*
  * Causal depthwise conv + LayerNorm + SiLU over B items of T frames:
  *
  *   out[b, t, c] = silu(LN_c(sum_{k<K} dwt[k, c] * g[b, t + k - (K-1), c]))

@@ -37,6 +37,10 @@ SIGNATURES = {
                                       ctypes.c_float, _VP, ctypes.c_int, ctypes.c_int, ctypes.c_int, _VP]),
     "sidon_glu": (ctypes.c_int, [_VP, _VP, ctypes.c_int, ctypes.c_int, _VP]),
     "sidon_silu": (ctypes.c_int, [_VP, ctypes.c_int64, _VP]),
+    "sidon_gemm_bias_act_fits": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int]),
+    "sidon_gemm_bias_act_preferred": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int]),
+    "sidon_gemm_bias_act": (ctypes.c_int, [_VP, ctypes.c_int, _VP, ctypes.c_int, _VP, _VP, ctypes.c_int,
+                                           ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _VP]),
     "sidon_causal_dw_norm": (ctypes.c_int, [_VP, ctypes.c_int, _VP, _VP, _VP, ctypes.c_float, _VP,
                                             ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _VP]),
     "sidon_fbank_frames": (ctypes.c_int, [_VP, _VP, ctypes.c_int, ctypes.c_int, _VP]),

@@ -17,7 +17,7 @@ from pathlib import Path
 PKG_DIR = Path(__file__).resolve().parent
 REPO_DIR = PKG_DIR.parent
 LIB_NAME = "libsidon_flexrel.so"
-SOURCES = [PKG_DIR / "csrc" / name for name in ("flexrel_fwd.hip", "res_norm.hip", "conformer_ops.hip", "fbank.hip")]
+SOURCES = [PKG_DIR / "csrc" / name for name in ("flexrel_fwd.hip", "res_norm.hip", "conformer_ops.hip", "fbank.hip", "gemm.hip")]
 ARCH = "gfx950"
 
 # -packed-fp32-ops: no v_pk_{add,mul,fma}_f32 in the generated code.

@@ -6,6 +6,10 @@ Same names and argument meaning as src/sidon_triton/triton_encoder.py:
   * ``causal_dw_norm(g, batch, dwt, ln_w, ln_b, eps)`` (:163-181): g [B*T, C]
     fp16, dwt [K, C] fp32 -> silu(LN(causal depthwise conv)) fp16;
   * ``silu_(h)``: the in-place F.silu of the feed-forward modules (:485-486);
+  * ``linear_silu(x, w, b)``: the feed-forward input projection and that SiLU
+    in one kernel (``silu_(torch.addmm(b, x, w.t()))`` up to the GEMM's
+    summation order; csrc/gemm.hip), for the shapes ``linear_silu_fits``
+    accepts (N a multiple of 256, K of 64);
 
 plus ``glu_causal_dw_norm(h, ...)``, the two fused: it reads the pointwise
 conv's output h [B*T, 2C] and forms g on the fly (bit-identical to
@@ -106,3 +110,48 @@ def glu_causal_dw_norm(h: torch.Tensor, batch: int, dwt: torch.Tensor, ln_w: tor
                        eps: float, out: torch.Tensor | None = None) -> torch.Tensor:
     """causal_dw_norm(glu(h), ...) in one pass: h [B*T, 2C] fp16."""
     return _dw(h, True, batch, dwt, ln_w, ln_b, eps, out)
+
+
+def linear_silu_fits(x: torch.Tensor, w: torch.Tensor) -> bool:
+    """Whether ``linear_silu`` takes x [M, K] and w [N, K]."""
+    return bool(_lib.load().sidon_gemm_bias_act_fits(x.shape[0], w.shape[0], w.shape[1])) and x.shape[1] == w.shape[1]
+
+
+def linear_silu_preferred(rows: int, n: int, k: int, device=None) -> bool:
+    """Whether ``linear_silu`` is expected to beat ``silu_(torch.addmm(...))``
+    for x [rows, k], w [n, k] on ``device`` (its tiles fill >= 3/4 of the CUs
+    in every round; at n = 4096, k = 1024 that is rows > 3840 on 256 CUs)."""
+    with torch.cuda.device(device):
+        return bool(_lib.load().sidon_gemm_bias_act_preferred(rows, n, k))
+
+
+def linear_silu(x: torch.Tensor, w: torch.Tensor, b: torch.Tensor | None, out: torch.Tensor | None = None,
+                act: bool = True) -> torch.Tensor:
+    """silu(fp16(x . w^T + b)) [M, N] fp16 for x [M, K] and w [N, K] fp16
+    (rows K-contiguous), b [N] fp16 or None; act=False leaves out the SiLU."""
+    device = x.device
+    for name, t in (("x", x), ("w", w)):
+        _check_device_tensor(name, t, device)
+        if t.dtype != torch.float16 or t.dim() != 2 or t.stride(1) != 1:
+            raise ValueError(f"{name} must be a float16 [rows, K] tensor with K contiguous")
+    rows, k = x.shape
+    n = w.shape[0]
+    if w.shape[1] != k:
+        raise ValueError(f"x has {k} columns, w {w.shape[1]}")
+    if b is not None:
+        _check_device_tensor("b", b, device)
+        if b.dtype != torch.float16 or tuple(b.shape) != (n,) or not b.is_contiguous():
+            raise ValueError(f"b must be a contiguous float16 [{n}] tensor")
+    if out is None:
+        out = torch.empty(rows, n, device=device, dtype=torch.float16)
+    else:
+        _check_device_tensor("out", out, device)
+        if out.dtype != torch.float16 or tuple(out.shape) != (rows, n) or out.stride(1) != 1:
+            raise ValueError(f"out must be a float16 [{rows}, {n}] tensor with rows contiguous")
+    lib = _lib.load()
+    with torch.cuda.device(device):
+        rc = lib.sidon_gemm_bias_act(x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0),
+                                     None if b is None else b.data_ptr(), out.data_ptr(), out.stride(0), rows, n, k,
+                                     1 if act else 0, _stream_handle(device))
+    _lib.check("sidon_gemm_bias_act", rc)
+    return out

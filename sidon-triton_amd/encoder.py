@@ -16,10 +16,12 @@ Mirrors src/sidon_triton/triton_encoder.py:
     ``load_encoder`` also reads the reference's own ``encoder_triton.pt``
     (with ``torch.load(weights_only=True)``).
 
-Per layer the work is: res_norm (HIP), hipBLASLt GEMMs through torch, SiLU
-(HIP, in place), the relative_key attention (HIP), and the conv module's
-GLU + causal depthwise conv + LayerNorm + SiLU as one HIP kernel reading the
-pointwise conv's output.  Every op launches on the current stream, reads no
+Per layer the work is: res_norm (HIP), hipBLASLt GEMMs through torch, the
+feed-forward input projections with bias and SiLU (one HIP GEMM kernel where
+its tiles fill the chip, else hipBLASLt followed by the in-place HIP SiLU),
+the relative_key attention (HIP), and the conv module's GLU + causal
+depthwise conv + LayerNorm + SiLU as one HIP kernel reading the pointwise
+conv's output.  Every op launches on the current stream, reads no
 device data on the host and, given a ``workspace``, allocates nothing, so a
 whole encoder call can be captured into one HIP graph per length bucket.
 """
@@ -31,7 +33,7 @@ from pathlib import Path
 
 import torch
 
-from .conformer import glu_causal_dw_norm, silu_
+from .conformer import glu_causal_dw_norm, linear_silu, linear_silu_preferred, silu_
 from .encoder_attention import flexrel_attention
 from .encoder_block import res_norm
 from .flexrel import HEAD_DIM, LEFT, NUM_POS, RIGHT
@@ -150,7 +152,10 @@ class HipEncoder:
     """fp32 features [B, L, F] (+ valid frames [B]) -> hidden [B, L, C] fp32 on
     packed weights (``pack_encoder`` / ``pack_weights``)."""
 
-    def __init__(self, packed: dict, device="cuda") -> None:
+    def __init__(self, packed: dict, device="cuda", fused_ffn: bool | None = None) -> None:
+        """fused_ffn: the feed-forward input projections as one GEMM + bias +
+        SiLU kernel (True), as hipBLASLt + SiLU (False), or chosen per call
+        by shape (None)."""
         device = torch.device(device)
         if device.type == "cuda" and device.index is None:
             device = torch.device("cuda", torch.cuda.current_device())
@@ -163,6 +168,7 @@ class HipEncoder:
         self.hidden = self.fp_w.shape[0]
         self.features = self.fp_w.shape[1]
         self.inter = self.layers[0]["ffn1_w1"].shape[0]
+        self.fused_ffn = fused_ffn
 
     def workspace(self, rows: int) -> dict:
         """Buffers for calls of up to ``rows`` = B*L rows (graph capture
@@ -212,6 +218,15 @@ class HipEncoder:
         layers = self.layers
         xn = res_norm(x, norm2=layers[0]["ffn1_ln"], write_x=False, xn=xn_buf)
 
+        fused = self.fused_ffn
+        if fused is None:
+            fused = linear_silu_preferred(rows, self.inter, hid, device)
+
+        def ffn_in(w, b):
+            if fused:
+                return linear_silu(xn, w, b, out=h_buf)
+            return silu_(torch.addmm(b, xn, w.t(), out=h_buf))
+
         def res(a, w, bias, **kw):
             torch.addmm(x, a, w.t(), out_dtype=torch.float32, out=x)
             return res_norm(x, bias=bias, xn=xn_buf if kw.get("norm2") is not None else None, **kw)
@@ -219,7 +234,7 @@ class HipEncoder:
         for i, p in enumerate(layers):
             b1, b2, b4 = p["cum_bias"]
             last = i + 1 == len(layers)
-            h = silu_(torch.addmm(p["ffn1_b1"], xn, p["ffn1_w1"].t(), out=h_buf))
+            h = ffn_in(p["ffn1_w1"], p["ffn1_b1"])
             xn = res(h, p["ffn1_w2"], b1, norm2=p["attn_ln"], write_x=False)
             qkv = torch.addmm(p["qkv_b"], xn, p["qkv_w"].t(), out=qkv_buf)
             c = flexrel_attention(qkv, batch, self.heads, p["rel"], lens, out=ctx)
@@ -227,7 +242,7 @@ class HipEncoder:
             pw1 = torch.mm(xn, p["pw1_w"].t(), out=pw1_buf)
             s = glu_causal_dw_norm(pw1, batch, p["dwt"], *p["dw_ln"], out=ctx)
             xn = res(s, p["pw2_w"], b2, norm2=p["ffn2_ln"], write_x=False)
-            h = silu_(torch.addmm(p["ffn2_b1"], xn, p["ffn2_w1"].t(), out=h_buf))
+            h = ffn_in(p["ffn2_w1"], p["ffn2_b1"])
             xn = res(h, p["ffn2_w2"], b4, norm1=p["final_ln"],
                      norm2=None if last else layers[i + 1]["ffn1_ln"])
         return x.view(batch, length, hid)

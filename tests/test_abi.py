@@ -109,3 +109,34 @@ def test_python_wrappers_reject_host_tensors(sidon):
         sidon.encoder_attention.flexrel_attention(qkv, 1, 2, rel, None)
     with pytest.raises(AssertionError):
         sidon.encoder_attention.flexrel_attention(qkv, 1, 2, torch.zeros(72, 64, dtype=torch.float16), None)
+
+
+def test_gemm_shape_support(sidon):
+    lib = sidon._lib.load()
+    assert lib.sidon_gemm_bias_act_fits(4800, 4096, 1024) == 1
+    assert lib.sidon_gemm_bias_act_fits(1, 256, 64) == 1
+    for m, n, k in ((0, 4096, 1024), (4800, 4000, 1024), (4800, 128, 1024), (4800, 4096, 1000), (4800, 4096, 32)):
+        assert lib.sidon_gemm_bias_act_fits(m, n, k) == 0, (m, n, k)
+
+
+@pytest.mark.parametrize("over,code", [
+    (dict(x=None), -1),
+    (dict(y=None), -1),
+    (dict(N=4000), -2),
+    (dict(K=1000), -2),
+    (dict(M=0), -2),
+    (dict(act=2), -2),
+    (dict(ldx=1000), -3),
+    (dict(ldy=4095), -3),
+    (dict(x=24), -4),
+    (dict(bias=12), -4),
+])
+def test_gemm_rejects_bad_arguments_before_launch(sidon, over, code):
+    # fake aligned addresses, never dereferenced: validation returns before any HIP call
+    lib = sidon._lib.load()
+    args = dict(x=16, ldx=1024, w=16, ldw=1024, bias=16, y=16, ldy=4096, M=4800, N=4096, K=1024, act=1)
+    args.update(over)
+    rc = lib.sidon_gemm_bias_act(args["x"], args["ldx"], args["w"], args["ldw"], args["bias"], args["y"],
+                                 args["ldy"], args["M"], args["N"], args["K"], args["act"], None)
+    assert rc == code
+    assert lib.sidon_last_error().decode()

@@ -1,0 +1,127 @@
+"""The fused feed-forward input projection (GEMM + bias + SiLU, csrc/gemm.hip)
+against float32 torch and against hipBLASLt followed by the in-place SiLU
+(needs an MI355X)."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+
+
+def _inputs(m, n, k, seed, ldx=None):
+    gen = torch.Generator().manual_seed(seed)
+    ldx = k if ldx is None else ldx
+    xs = torch.randn(m, ldx, generator=gen).half().to(DEV)
+    w = (torch.randn(n, k, generator=gen) / k ** 0.5).half().to(DEV)
+    b = (torch.randn(n, generator=gen) * 0.1).half().to(DEV)
+    return xs[:, :k], w, b
+
+
+def _reference(x, w, b, act):
+    """fp32 sums, bias added, rounded to fp16 (as addmm stores it), SiLU in
+    fp32, rounded to fp16."""
+    h = x.float() @ w.float().t()
+    if b is not None:
+        h = h + b.float()
+    h = h.half().float()
+    return (torch.nn.functional.silu(h) if act else h).half()
+
+
+@pytest.mark.parametrize("m,n,k,bias,act,ldx", [
+    (4800, 4096, 1024, True, True, None),
+    (1000, 512, 256, True, True, None),
+    (333, 256, 64, False, False, None),
+    (1, 256, 128, True, True, None),
+    (650, 768, 128, True, True, 192),
+])
+def test_linear_silu_matches_fp32(sidon, m, n, k, bias, act, ldx):
+    x, w, b = _inputs(m, n, k, seed=m + n + k, ldx=ldx)
+    b = b if bias else None
+    got = sidon.conformer.linear_silu(x, w, b, act=act)
+    ref = _reference(x, w, b, act)
+    torch.cuda.synchronize()
+    err = (got.float() - ref.float()).abs()
+    # the fp32 sums differ from torch's only in summation order: at most one
+    # fp16 rounding step apart after the final rounding
+    tol = 2e-3 + 2e-3 * ref.float().abs()
+    assert torch.isfinite(got.float()).all()
+    assert (err <= tol).all(), float(err.max())
+    snr = 10 * torch.log10(ref.float().pow(2).sum() / (got.float() - ref.float()).pow(2).sum().clamp_min(1e-30))
+    assert snr > 60, float(snr)
+
+
+def test_linear_silu_matches_library_gemm_then_silu(sidon):
+    """Same shape as the encoder's FFN input at a 96 s chunk; hipBLASLt's GEMM
+    plus the in-place SiLU agree to within one fp16 rounding (measured: bit for bit)."""
+    x, w, b = _inputs(4800, 4096, 1024, seed=7)
+    fused = sidon.conformer.linear_silu(x, w, b)
+    twostep = sidon.conformer.silu_(torch.addmm(b, x, w.t()))
+    torch.cuda.synchronize()
+    diff = (fused.float() - twostep.float()).abs()
+    print(f"fused vs two-step: max {float(diff.max()):.3e}, differing {float((diff > 0).float().mean()):.4f}")
+    assert torch.allclose(fused.float(), twostep.float(), atol=2e-3, rtol=2e-3)
+
+
+def test_linear_silu_out_buffer_and_strides(sidon):
+    """A strided output view: untouched columns stay untouched."""
+    x, w, b = _inputs(500, 256, 128, seed=11)
+    big = torch.full((500, 512), 5.0, dtype=torch.float16, device=DEV)
+    out = big[:, 128:384]
+    sidon.conformer.linear_silu(x, w, b, out=out)
+    torch.cuda.synchronize()
+    assert torch.all(big[:, :128] == 5.0) and torch.all(big[:, 384:] == 5.0)
+    assert torch.allclose(out.float(), _reference(x, w, b, True).float(), atol=2e-3, rtol=2e-3)
+
+
+def test_encoder_fused_and_library_ffn_agree(sidon):
+    """The whole encoder at Sidon's full width (8 layers, L=750) with the fused
+    FFN input kernel forced on and forced off, and the fused one against the
+    fp32 torch oracle."""
+    import bench
+    from oracle.encoder_oracle import encoder_reference
+    from oracle.flexrel_oracle import errors
+
+    weights = bench.encoder_model_weights(torch, seed=7, device=DEV)
+    packed = sidon.encoder.pack_weights(weights)
+    gen = torch.Generator().manual_seed(750)
+    feats = torch.randn(1, 750, 160, generator=gen).to(DEV)
+    frames = torch.tensor([750], dtype=torch.int32, device=DEV)
+    on = sidon.encoder.HipEncoder(packed, DEV, fused_ffn=True)(feats, frames)
+    off = sidon.encoder.HipEncoder(packed, DEV, fused_ffn=False)(feats, frames)
+    torch.cuda.synchronize()
+    agree = errors(off[0].double().cpu().numpy(), on[0].double().cpu().numpy())
+    want = encoder_reference(feats, weights, [750], dtype=torch.float32)
+    err = errors(want[0].double().cpu().numpy(), on[0].double().cpu().numpy())
+    print("fused vs library FFN input:", agree, "fused vs fp32 oracle:", err)
+    assert torch.isfinite(on).all()
+    assert agree["snr_db"] > 80, agree
+    assert err["snr_db"] > 58 and err["max_abs"] < 0.02 * want.abs().max().item(), err
+
+
+def test_linear_silu_graph_replays_match_eager(sidon):
+    """Captured into a HIP graph and replayed three times, with eager work and
+    synchronisations between the replays: every replay equals the eager call."""
+    x, w, b = _inputs(4800, 4096, 1024, seed=13)
+    out = torch.empty(4800, 4096, dtype=torch.float16, device=DEV)
+    sidon.conformer.linear_silu(x, w, b, out=out)
+    torch.cuda.synchronize()
+    eager = out.clone()
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        sidon.conformer.linear_silu(x, w, b, out=out)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph):
+        sidon.conformer.linear_silu(x, w, b, out=out)
+    for rep in range(3):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), rep
+        _ = (x.float() * 2).sum().item()  # unrelated eager work
