@@ -100,8 +100,8 @@ __device__ __forceinline__ void dma_1k(uint32_t lds_addr, const char* gbase, uin
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() { asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory"); }
 
-// Wait until slice kt has landed while up to `newer` later slices (of
-// `per` copies each) stay in flight.
+// Wait until slice kt has landed while up to `newer` later slices (of kPer
+// copies each, issued after it by this wavefront) stay in flight.
 template <int kPer>
 __device__ __forceinline__ void wait_slice(int newer) {
   if (newer >= 2) {
@@ -144,10 +144,10 @@ __global__ void __launch_bounds__(kThreads) gemm_bias_act_kernel(const GemmParam
   const int m0 = tm * kTileM;
   const int n0 = tn * kTileN;
 
-  // Copy instruction i (of 36 per slice; wavefront w issues i = w + 8 j):
-  // rows 16 i' + lane / 4 of the X slice (i < 20) or of the W slice; lane
-  // offsets fixed for the whole loop (X rows >= M re-read row M - 1, whose
-  // results are never stored).
+  // Copy instruction i (of kCopies per slice; wavefront w issues i = w + 8 j):
+  // rows kRowsPerCopy i' + lane / kChunks of the X slice (i < kCopiesA) or of
+  // the W slice; lane offsets fixed for the whole loop (X rows >= M re-read
+  // row M - 1, whose results are never stored).
   const uint32_t lds0 = (uint32_t)(uintptr_t)LDS_PTR(char, smem);
   uint32_t voff[kCopySlots];
 #pragma unroll
@@ -159,7 +159,7 @@ __global__ void __launch_bounds__(kThreads) gemm_bias_act_kernel(const GemmParam
     voff[j] = xi ? (uint32_t)min(m0 + r, p.M - 1) * (uint32_t)p.ldx * 2u + (uint32_t)c * 16u
                  : (uint32_t)(n0 + r) * (uint32_t)p.ldw * 2u + (uint32_t)c * 16u;
   }
-  const char* xg = reinterpret_cast<const char*>(p.x);  // (wait_slice below counts these copies)
+  const char* xg = reinterpret_cast<const char*>(p.x);
   const char* wg = reinterpret_cast<const char*>(p.w);
   auto issue = [&](int kt) {
     const uint32_t base = lds0 + (kt % kStages) * kStage;
@@ -196,7 +196,7 @@ __global__ void __launch_bounds__(kThreads) gemm_bias_act_kernel(const GemmParam
     if (kt < kslices) issue(kt);
   for (int kt = 0; kt < kslices; ++kt) {
     // Slice kt has landed for every wavefront, and nobody reads slice kt - 1
-    // any more, whose buffer the copy of slice kt + 3 refills.
+    // any more, whose buffer the copy of slice kt + kStages - 1 refills.
     const int newer = min(kStages - 2, kslices - 1 - kt);
     if (w < kFullWaves) {
       wait_slice<kCopySlots>(newer);
