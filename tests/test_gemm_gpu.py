@@ -125,3 +125,23 @@ def test_linear_silu_graph_replays_match_eager(sidon):
         torch.cuda.synchronize()
         assert torch.equal(out, eager), rep
         _ = (x.float() * 2).sum().item()  # unrelated eager work
+
+
+def test_runtime_full_chunk_graph_replays_match_eager(sidon):
+    """The encoder runtime at a full 96 s chunk (the fused FFN input kernel's
+    shape): graph replays, with eager work between them, equal eager calls."""
+    import bench
+
+    weights = bench.encoder_model_weights(torch, seed=5, device=DEV)
+    enc = sidon.encoder.HipEncoder(sidon.encoder.pack_weights(weights), DEV)
+    assert sidon.conformer.linear_silu_preferred(4800, enc.inter, enc.hidden, DEV)
+    rt = sidon.runtime.EncoderRuntime(enc, max_batch=1, max_seconds=96, max_graphs=2)
+    gen = torch.Generator().manual_seed(6)
+    for rep, frames in enumerate((4800, 4731, 4800)):
+        feats = torch.randn(1, 4800, 160, generator=gen)
+        got = rt.run(feats, [frames]).clone()
+        want = enc(feats.to(DEV), torch.tensor([frames], dtype=torch.int32, device=DEV))
+        torch.cuda.synchronize()
+        assert torch.equal(got[0, :frames], want[0, :frames]), rep
+        _ = (want * 2).sum().item()  # unrelated eager work between replays
+    assert len(rt.graphs) == 1
