@@ -102,7 +102,7 @@ int sidon_flexrel_launch_shape(int B, int H, int L, int* queries_per_block,
 /* Thread-local text of the last error ("" when none). */
 const char* sidon_last_error(void);
 
-/* Library version string, e.g. "sidon-flexrel 0.1.0 gfx950". */
+/* Library version string, e.g. "sidon-flexrel 0.3.0 gfx950". */
 const char* sidon_version(void);
 
 #ifdef __cplusplus

@@ -922,4 +922,4 @@ SIDON_API int sidon_flexrel_fwd_qkv(const void* qkv, const void* rel, const int3
 
 SIDON_API const char* sidon_last_error(void) { return sidon::g_err; }
 
-SIDON_API const char* sidon_version(void) { return "sidon-flexrel 0.2.0 gfx950"; }
+SIDON_API const char* sidon_version(void) { return "sidon-flexrel 0.3.0 gfx950"; }
