@@ -235,7 +235,7 @@ flexrel_fwd_kernel(const Params p) {
   const int64_t vstride = (int64_t)p.vsl * 2;
 
   // Key steps: T steps of 32 keys cover [0, LK); this wavefront takes steps
-  // w + 4 u, u = 0 .. nu - 1.
+  // w + 8 u, u = 0 .. nu - 1.
   const int T = (LK + kStep - 1) / kStep;
   const int nu = T > w ? (T - w + kWaves - 1) / kWaves : 0;
   const bool active = nu > 0;
