@@ -40,12 +40,13 @@ constexpr int kFramesPerBlock = 4;   // logmel: one wavefront each
 constexpr int kLanes = 4;            // normalize: frame lanes x 80 bins per block
 constexpr int kApplyFrames = 64;     // normalize: frames per apply block
 constexpr int kMaxTiles = 64;
+constexpr int kMergeThreads = 1024;  // merge: threads per item (loads), the first 80 merge
 
 // frames[b, f, i] = chunk[b, 160 f + i - 160] (zero outside [0, S)): the
 // (160, 160) edge padding and the 400 / 160 framing in one pass, 4 samples
 // per thread.
 __global__ void __launch_bounds__(256) frames_kernel(const float* __restrict__ chunk, float* __restrict__ frames,
-                                                    int S, int F, int64_t total4) {
+                                                    int S, int F, int64_t total4, bool vec4) {
   const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (q >= total4) return;
   const int64_t e = q * 4;                       // element of [B, F, 400]
@@ -56,10 +57,14 @@ __global__ void __launch_bounds__(256) frames_kernel(const float* __restrict__ c
   const int t0 = f * kFrameShift + i - kEdgePad;
   const float* src = chunk + b * S;
   float4 v;
-  v.x = (t0 >= 0 && t0 < S) ? src[t0] : 0.f;
-  v.y = (t0 + 1 >= 0 && t0 + 1 < S) ? src[t0 + 1] : 0.f;
-  v.z = (t0 + 2 >= 0 && t0 + 2 < S) ? src[t0 + 2] : 0.f;
-  v.w = (t0 + 3 >= 0 && t0 + 3 < S) ? src[t0 + 3] : 0.f;
+  if (t0 >= 0 && t0 + 3 < S && vec4) {
+    v = *reinterpret_cast<const float4*>(src + t0);  // t0 % 4 == 0; rows 16-byte aligned
+  } else {
+    v.x = (t0 >= 0 && t0 < S) ? src[t0] : 0.f;
+    v.y = (t0 + 1 >= 0 && t0 + 1 < S) ? src[t0 + 1] : 0.f;
+    v.z = (t0 + 2 >= 0 && t0 + 2 < S) ? src[t0 + 2] : 0.f;
+    v.w = (t0 + 3 >= 0 && t0 + 3 < S) ? src[t0 + 3] : 0.f;
+  }
   *reinterpret_cast<float4*>(frames + e) = v;
 }
 
@@ -141,28 +146,76 @@ __global__ void __launch_bounds__(kLanes * kMel) stats_kernel(const float* __res
 // Block b: merge item b's tile sums in tile order (Chan et al.'s pairwise
 // update of count, mean and sum of squared deviations) from LDS; writes
 // (mean, sqrt(var + eps)) per bin after the partials.
-__global__ void __launch_bounds__(256) merge_kernel(const int* __restrict__ valid, float* __restrict__ part, int F,
-                                                   int G, int B) {
-  __shared__ float sp[kMaxTiles * kMel * 3];
+__global__ void __launch_bounds__(kMergeThreads) merge_kernel(const int* __restrict__ valid, float* __restrict__ part,
+                                                             int F, int G, int B) {
+  __shared__ __attribute__((aligned(16))) float sp[kMaxTiles * kMel * 3];
   const int b = blockIdx.x;
   const float* src = part + (int64_t)b * G * kMel * 3;
-#pragma unroll 8
-  for (int i = threadIdx.x; i < G * kMel * 3; i += 256) sp[i] = src[i];
+  // The tiles' partial statistics into LDS with every load in flight at once
+  // (one memory latency, not one per batch of loads).
+  const int nval = G * kMel * 3;  // a multiple of 4
+  if ((reinterpret_cast<uintptr_t>(src) & 15) == 0) {
+    constexpr int kPer = (kMaxTiles * kMel * 3 / 4 + kMergeThreads - 1) / kMergeThreads;
+    float4 v[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int i = threadIdx.x + kMergeThreads * j;
+      if (i < nval / 4) v[j] = reinterpret_cast<const float4*>(src)[i];
+    }
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int i = threadIdx.x + kMergeThreads * j;
+      if (i < nval / 4) reinterpret_cast<float4*>(sp)[i] = v[j];
+    }
+  } else {
+    constexpr int kPer = (kMaxTiles * kMel * 3 + kMergeThreads - 1) / kMergeThreads;
+    float v[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int i = threadIdx.x + kMergeThreads * j;
+      if (i < nval) v[j] = src[i];
+    }
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int i = threadIdx.x + kMergeThreads * j;
+      if (i < nval) sp[i] = v[j];
+    }
+  }
   __syncthreads();
+  // Pairwise tree over the tiles, the same for every call (deterministic):
+  // level l merges tile g + 2^l into tile g for g a multiple of 2^(l+1),
+  // with the pairwise update of count, mean and M2 (Chan et al.).
+  for (int stride = 1; stride < G; stride *= 2) {
+    const int pairs = (G + 2 * stride - 1) / (2 * stride);
+    for (int t = threadIdx.x; t < pairs * kMel; t += kMergeThreads) {
+      const int mm = t % kMel;
+      const int g = (t / kMel) * 2 * stride;
+      if (g + stride < G) {
+        float* a = sp + (g * kMel + mm) * 3;
+        const float* c = sp + ((g + stride) * kMel + mm) * 3;
+        const float na = a[0], nb = c[0];
+        if (nb > 0.f) {
+          if (na <= 0.f) {
+            a[0] = nb;
+            a[1] = c[1];
+            a[2] = c[2];
+          } else {
+            const float nt = na + nb;
+            const float d = c[1] - a[1];
+            a[1] += d * (nb / nt);
+            a[2] += c[2] + d * d * (na * nb / nt);
+            a[0] = nt;
+          }
+        }
+      }
+    }
+    __syncthreads();
+  }
   const int m = threadIdx.x;
   if (m >= kMel) return;
   const int tf = true_frames(valid[b], F);
-  float n = 0.f, mean = 0.f, m2 = 0.f;
-  for (int g = 0; g < G; ++g) {
-    const float* p = sp + (g * kMel + m) * 3;
-    const float nb = p[0];
-    if (nb <= 0.f) continue;
-    const float nt = n + nb;
-    const float d = p[1] - mean;
-    mean += d * (nb / nt);
-    m2 += p[2] + d * d * (n * nb / nt);
-    n = nt;
-  }
+  const float mean = sp[m * 3 + 1];
+  const float m2 = sp[m * 3 + 2];
   float* stats = part + (int64_t)B * G * kMel * 3 + ((int64_t)b * kMel + m) * 2;
   stats[0] = mean;
   stats[1] = sqrtf(m2 / (float)(tf - 1) + kVarEps);
@@ -183,16 +236,21 @@ __global__ void __launch_bounds__(kLanes * kMel) apply_kernel(const float* __res
   const float* xb = x + (int64_t)b * F * kMel;
   float* ob = out + (int64_t)b * F * kMel;
   const int fbase = blockIdx.x * kApplyFrames;
-  for (int i = fl; i < kApplyFrames; i += kLanes) {
-    const int f = fbase + i;
-    if (f >= F) break;
-    float v;
-    if (f < tf) {
-      v = (xb[(int64_t)f * kMel + m] - mean) / denom;
-    } else {
-      v = (f == tf && (tf & 1)) ? kPadValue : 0.f;
+  // All of the thread's loads first (one memory latency), then the stores.
+  constexpr int kPer = kApplyFrames / kLanes;
+  float x_in[kPer];
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int f = fbase + fl + kLanes * j;
+    x_in[j] = f < tf ? xb[(int64_t)f * kMel + m] : 0.f;  // tf <= F
+  }
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int f = fbase + fl + kLanes * j;
+    if (f < F) {
+      const float v = f < tf ? (x_in[j] - mean) / denom : ((f == tf && (tf & 1)) ? kPadValue : 0.f);
+      ob[(int64_t)f * kMel + m] = v;
     }
-    ob[(int64_t)f * kMel + m] = v;
   }
 }
 
@@ -227,8 +285,11 @@ SIDON_API int sidon_fbank_frames(const float* chunk, float* frames, int B, int S
   if ((rc = sidon::check_device())) return rc;
   const int F = S / kFrameShift;
   const int64_t total4 = (int64_t)B * F * kFrameSize / 4;
+  // 16-byte source loads when every item's row starts 16-byte aligned (S is a
+  // multiple of 320, so that holds when the chunk pointer is aligned).
+  const bool vec4 = sidon::aligned16(chunk);
   hipLaunchKernelGGL(frames_kernel, dim3((unsigned)((total4 + 255) / 256)), dim3(256), 0,
-                     reinterpret_cast<hipStream_t>(stream), chunk, frames, S, F, total4);
+                     reinterpret_cast<hipStream_t>(stream), chunk, frames, S, F, total4, vec4);
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) return fail(SIDON_E_LAUNCH, "fbank frames launch failed: %s", hipGetErrorString(err));
   return SIDON_OK;
@@ -256,7 +317,7 @@ SIDON_API int sidon_fbank_normalize(const float* logmel, const int* valid, float
   hipLaunchKernelGGL(stats_kernel, dim3(G, B), dim3(kLanes * kMel), 0, s, logmel, valid, workspace, F, G);
   hipError_t err = hipGetLastError();
   if (err == hipSuccess) {
-    hipLaunchKernelGGL(merge_kernel, dim3(B), dim3(256), 0, s, valid, workspace, F, G, B);
+    hipLaunchKernelGGL(merge_kernel, dim3(B), dim3(kMergeThreads), 0, s, valid, workspace, F, G, B);
     err = hipGetLastError();
   }
   if (err == hipSuccess) {
