@@ -12,7 +12,7 @@
 // logmel: one wavefront per frame; the 257 powers go to LDS, then lane m sums
 // the nonzero span of mel triangle m (sparse: start bin, length, weights).
 // normalize: statistics are per-tile two-pass sums (fixed tiles of frames,
-// one block per (tile, item)), merged in tile order by one block per item --
+// one block per (tile, item)), merged by a fixed pairwise tree in one block per item --
 // deterministic, no atomics -- through a caller-provided workspace; a third
 // kernel applies them to every frame.  frames: the edge padding and framing
 // that feed the framing GEMM.
@@ -40,7 +40,7 @@ constexpr int kFramesPerBlock = 4;   // logmel: one wavefront each
 constexpr int kLanes = 4;            // normalize: frame lanes x 80 bins per block
 constexpr int kApplyFrames = 64;     // normalize: frames per apply block
 constexpr int kMaxTiles = 64;
-constexpr int kMergeThreads = 1024;  // merge: threads per item (loads), the first 80 merge
+constexpr int kMergeThreads = 1024;  // merge: threads per item
 
 // frames[b, f, i] = chunk[b, 160 f + i - 160] (zero outside [0, S)): the
 // (160, 160) edge padding and the 400 / 160 framing in one pass, 4 samples
@@ -143,8 +143,8 @@ __global__ void __launch_bounds__(kLanes * kMel) stats_kernel(const float* __res
   }
 }
 
-// Block b: merge item b's tile sums in tile order (Chan et al.'s pairwise
-// update of count, mean and sum of squared deviations) from LDS; writes
+// Block b: merge item b's tile sums by a fixed pairwise tree (Chan et al.'s
+// update of count, mean and sum of squared deviations) in LDS; writes
 // (mean, sqrt(var + eps)) per bin after the partials.
 __global__ void __launch_bounds__(kMergeThreads) merge_kernel(const int* __restrict__ valid, float* __restrict__ part,
                                                              int F, int G, int B) {
