@@ -78,11 +78,20 @@ __global__ void __launch_bounds__(64 * kFramesPerBlock) logmel_kernel(const floa
   const int w = threadIdx.x >> 6;
   const int r = blockIdx.x * kFramesPerBlock + w;
   if (r < R) {
+    // All of the lane's loads in flight together (unrolled, guarded).
     const float* row = spec + (int64_t)r * kSpecWidth;
-    for (int k = lane; k < kBins; k += 64) {
-      const float re = row[k];
-      const float im = row[kBins + k];
-      power[w][k] = re * re + im * im;
+    constexpr int kPer = (kBins + 63) / 64;
+    float re[kPer], im[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int k = lane + 64 * j;
+      re[j] = k < kBins ? row[k] : 0.f;
+      im[j] = k < kBins ? row[kBins + k] : 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int k = lane + 64 * j;
+      if (k < kBins) power[w][k] = re[j] * re[j] + im[j] * im[j];
     }
   }
   __syncthreads();
@@ -92,6 +101,9 @@ __global__ void __launch_bounds__(64 * kFramesPerBlock) logmel_kernel(const floa
     const int n = mel_len[m];
     const float* wm = mel_w + m * max_len;
     float acc = 0.f;
+    // (unrolled so that several weight loads are in flight; the sum keeps
+    // its order i = 0 .. n - 1)
+#pragma unroll 8
     for (int i = 0; i < n; ++i) acc = fmaf(wm[i], power[w][lo + i], acc);
     out[(int64_t)r * kMel + m] = logf(fmaxf(acc, kMelFloor));
   }
