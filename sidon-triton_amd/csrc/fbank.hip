@@ -40,6 +40,7 @@ constexpr int kFramesPerBlock = 4;   // logmel: one wavefront each
 constexpr int kLanes = 4;            // normalize: frame lanes x 80 bins per block
 constexpr int kApplyFrames = 64;     // normalize: frames per apply block
 constexpr int kMaxTiles = 64;
+constexpr int kStatsCache = 40;      // statistics: frames per lane held in registers
 constexpr int kMergeThreads = 1024;  // merge: threads per item
 
 // frames[b, f, i] = chunk[b, 160 f + i - 160] (zero outside [0, S)): the
@@ -132,18 +133,44 @@ __global__ void __launch_bounds__(kLanes * kMel) stats_kernel(const float* __res
   const int f1 = min(f0 + per, tf);
   const int n = max(f1 - f0, 0);
   const float* xb = x + (int64_t)b * F * kMel;
+  // Tiles of up to kLanes * kStatsCache frames are held in registers, loaded
+  // in one round (one memory latency for both passes); longer tiles stream.
+  // Either way the sums run over f = f0 + fl, f0 + fl + kLanes, ... in order.
+  const int nl = f1 > f0 + fl ? (f1 - f0 - fl + kLanes - 1) / kLanes : 0;
+  float xv[kStatsCache];
+  const bool cached = nl <= kStatsCache;
+  if (cached) {
+#pragma unroll
+    for (int j = 0; j < kStatsCache; ++j) xv[j] = j < nl ? xb[(int64_t)(f0 + fl + kLanes * j) * kMel + m] : 0.f;
+  }
   float s = 0.f;
+  if (cached) {
+#pragma unroll
+    for (int j = 0; j < kStatsCache; ++j)
+      if (j < nl) s += xv[j];
+  } else {
 #pragma unroll 8
-  for (int f = f0 + fl; f < f1; f += kLanes) s += xb[(int64_t)f * kMel + m];
+    for (int f = f0 + fl; f < f1; f += kLanes) s += xb[(int64_t)f * kMel + m];
+  }
   red[fl][m] = s;
   __syncthreads();
   const float mean = n > 0 ? ((red[0][m] + red[1][m]) + (red[2][m] + red[3][m])) / (float)n : 0.f;
   __syncthreads();
   float q = 0.f;
+  if (cached) {
+#pragma unroll
+    for (int j = 0; j < kStatsCache; ++j) {
+      if (j < nl) {
+        const float d = xv[j] - mean;
+        q = fmaf(d, d, q);
+      }
+    }
+  } else {
 #pragma unroll 8
-  for (int f = f0 + fl; f < f1; f += kLanes) {
-    const float d = xb[(int64_t)f * kMel + m] - mean;
-    q = fmaf(d, d, q);
+    for (int f = f0 + fl; f < f1; f += kLanes) {
+      const float d = xb[(int64_t)f * kMel + m] - mean;
+      q = fmaf(d, d, q);
+    }
   }
   red[fl][m] = q;
   __syncthreads();
