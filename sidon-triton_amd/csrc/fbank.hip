@@ -12,7 +12,7 @@
 // logmel: one wavefront per frame; the 257 powers go to LDS, then lane m sums
 // the nonzero span of mel triangle m (sparse: start bin, length, weights).
 // normalize: statistics are per-tile two-pass sums (fixed tiles of frames,
-// one block per (tile, item)), merged by a fixed pairwise tree in one block per item --
+// one block per (tile, item)), merged by a fixed pairwise tree, one block per (bin group, item) --
 // deterministic, no atomics -- through a caller-provided workspace; a third
 // kernel applies them to every frame.  frames: the edge padding and framing
 // that feed the framing GEMM.
@@ -41,7 +41,8 @@ constexpr int kLanes = 4;            // normalize: frame lanes x 80 bins per blo
 constexpr int kApplyFrames = 64;     // normalize: frames per apply block
 constexpr int kMaxTiles = 64;
 constexpr int kStatsCache = 40;      // statistics: frames per lane held in registers
-constexpr int kMergeThreads = 1024;  // merge: threads per item
+constexpr int kMergeBins = 10;       // merge: mel bins per block (8 blocks per item)
+constexpr int kMergeThreads = 320;   // merge: threads per block (32 tile pairs x 10 bins)
 
 // frames[b, f, i] = chunk[b, 160 f + i - 160] (zero outside [0, S)): the
 // (160, 160) edge padding and the 400 / 160 framing in one pass, 4 samples
@@ -182,56 +183,45 @@ __global__ void __launch_bounds__(kLanes * kMel) stats_kernel(const float* __res
   }
 }
 
-// Block b: merge item b's tile sums by a fixed pairwise tree (Chan et al.'s
-// update of count, mean and sum of squared deviations) in LDS; writes
-// (mean, sqrt(var + eps)) per bin after the partials.
+// Block (bin group, item b): merge item b's tile sums of kMergeBins bins by
+// a fixed pairwise tree (Chan et al.'s update of count, mean and sum of
+// squared deviations) in LDS; writes (mean, sqrt(var + eps)) per bin after
+// the partials.
 __global__ void __launch_bounds__(kMergeThreads) merge_kernel(const int* __restrict__ valid, float* __restrict__ part,
                                                              int F, int G, int B) {
-  __shared__ __attribute__((aligned(16))) float sp[kMaxTiles * kMel * 3];
-  const int b = blockIdx.x;
-  const float* src = part + (int64_t)b * G * kMel * 3;
-  // The tiles' partial statistics into LDS with every load in flight at once
-  // (one memory latency, not one per batch of loads).
-  const int nval = G * kMel * 3;  // a multiple of 4
-  if ((reinterpret_cast<uintptr_t>(src) & 15) == 0) {
-    constexpr int kPer = (kMaxTiles * kMel * 3 / 4 + kMergeThreads - 1) / kMergeThreads;
-    float4 v[kPer];
-#pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-      const int i = threadIdx.x + kMergeThreads * j;
-      if (i < nval / 4) v[j] = reinterpret_cast<const float4*>(src)[i];
-    }
-#pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-      const int i = threadIdx.x + kMergeThreads * j;
-      if (i < nval / 4) reinterpret_cast<float4*>(sp)[i] = v[j];
-    }
-  } else {
-    constexpr int kPer = (kMaxTiles * kMel * 3 + kMergeThreads - 1) / kMergeThreads;
+  constexpr int kVals = kMergeBins * 3;  // floats per tile of this group
+  __shared__ float sp[kMaxTiles * kVals];
+  const int b = blockIdx.y;
+  const int m0 = blockIdx.x * kMergeBins;
+  const float* src = part + (int64_t)b * G * kMel * 3 + m0 * 3;
+  // The group's partials into LDS, every load in flight at once (one memory
+  // latency): tile g's kVals floats sit at src + g * kMel * 3.
+  {
+    constexpr int kPer = (kMaxTiles * kVals + kMergeThreads - 1) / kMergeThreads;
     float v[kPer];
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {
       const int i = threadIdx.x + kMergeThreads * j;
-      if (i < nval) v[j] = src[i];
+      const int g = i / kVals;
+      v[j] = g < G ? src[(int64_t)g * kMel * 3 + (i - g * kVals)] : 0.f;
     }
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {
       const int i = threadIdx.x + kMergeThreads * j;
-      if (i < nval) sp[i] = v[j];
+      if (i / kVals < G) sp[i] = v[j];
     }
   }
   __syncthreads();
   // Pairwise tree over the tiles, the same for every call (deterministic):
-  // level l merges tile g + 2^l into tile g for g a multiple of 2^(l+1),
-  // with the pairwise update of count, mean and M2 (Chan et al.).
+  // level l merges tile g + 2^l into tile g for g a multiple of 2^(l+1).
   for (int stride = 1; stride < G; stride *= 2) {
     const int pairs = (G + 2 * stride - 1) / (2 * stride);
-    for (int t = threadIdx.x; t < pairs * kMel; t += kMergeThreads) {
-      const int mm = t % kMel;
-      const int g = (t / kMel) * 2 * stride;
+    for (int t = threadIdx.x; t < pairs * kMergeBins; t += kMergeThreads) {
+      const int mm = t % kMergeBins;
+      const int g = (t / kMergeBins) * 2 * stride;
       if (g + stride < G) {
-        float* a = sp + (g * kMel + mm) * 3;
-        const float* c = sp + ((g + stride) * kMel + mm) * 3;
+        float* a = sp + g * kVals + mm * 3;
+        const float* c = sp + (g + stride) * kVals + mm * 3;
         const float na = a[0], nb = c[0];
         if (nb > 0.f) {
           if (na <= 0.f) {
@@ -250,12 +240,12 @@ __global__ void __launch_bounds__(kMergeThreads) merge_kernel(const int* __restr
     }
     __syncthreads();
   }
-  const int m = threadIdx.x;
-  if (m >= kMel) return;
+  const int mm = threadIdx.x;
+  if (mm >= kMergeBins) return;
   const int tf = true_frames(valid[b], F);
-  const float mean = sp[m * 3 + 1];
-  const float m2 = sp[m * 3 + 2];
-  float* stats = part + (int64_t)B * G * kMel * 3 + ((int64_t)b * kMel + m) * 2;
+  const float mean = sp[mm * 3 + 1];
+  const float m2 = sp[mm * 3 + 2];
+  float* stats = part + (int64_t)B * G * kMel * 3 + ((int64_t)b * kMel + m0 + mm) * 2;
   stats[0] = mean;
   stats[1] = sqrtf(m2 / (float)(tf - 1) + kVarEps);
 }
@@ -356,7 +346,7 @@ SIDON_API int sidon_fbank_normalize(const float* logmel, const int* valid, float
   hipLaunchKernelGGL(stats_kernel, dim3(G, B), dim3(kLanes * kMel), 0, s, logmel, valid, workspace, F, G);
   hipError_t err = hipGetLastError();
   if (err == hipSuccess) {
-    hipLaunchKernelGGL(merge_kernel, dim3(B), dim3(kMergeThreads), 0, s, valid, workspace, F, G, B);
+    hipLaunchKernelGGL(merge_kernel, dim3(kMel / kMergeBins, B), dim3(kMergeThreads), 0, s, valid, workspace, F, G, B);
     err = hipGetLastError();
   }
   if (err == hipSuccess) {

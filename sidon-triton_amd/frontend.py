@@ -122,7 +122,9 @@ class Fbank:
         if device.type == "cuda" and device.index is None:
             device = torch.device("cuda", torch.cuda.current_device())
         self.device = device
-        self.weight = frame_transform().float().to(device)
+        # Kept as [514, 400] and used transposed: hipBLASLt picks a faster kernel
+        # for this operand order (57.5 against 59.6 us at a 96 s chunk).
+        self.weight_t = frame_transform().float().t().contiguous().to(device)
         lo, length, weights = sparse_mel(mel_banks())
         self.mel_lo = torch.from_numpy(lo).to(device)
         self.mel_len = torch.from_numpy(length).to(device)
@@ -170,7 +172,7 @@ class Fbank:
             rc = lib.sidon_fbank_frames(chunk.data_ptr(), fr.data_ptr(), batch, samples, stream)
         _lib.check("sidon_fbank_frames", rc)
         spec = ws["spec"][:batch * frames * 2 * N_BINS].view(batch * frames, 2 * N_BINS)
-        torch.mm(fr, self.weight, out=spec)
+        torch.mm(fr, self.weight_t.t(), out=spec)
         logmel = ws["logmel"][:batch * frames * NUM_MEL]
         if out is None:
             out = torch.empty(batch, frames // 2, 2 * NUM_MEL, device=device)
