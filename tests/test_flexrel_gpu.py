@@ -184,6 +184,43 @@ def test_growing_scores_force_max_updates(sidon, direction):
     assert_parity(ref, got, [1037], f"ramp{direction}")
 
 
+def test_equal_table_rows_match_sdpa(sidon):
+    """Every row of E equal: the bias q.e is one constant per query row, which
+    the softmax cancels, so the output is plain attention (torch SDPA, fp32,
+    CPU).  At L=700 every query block has left, band and right steps, so the
+    two side constants and the band gather all carry the same shift."""
+    q, k, v, _ = seeded_inputs(1, 4, 700, seed=53)
+    row = torch.randn(1, 64, generator=torch.Generator().manual_seed(54)) * 2.0
+    rel = row.expand(73, 64).contiguous().half()
+    got = run(sidon, q, k, v, rel, [661]).float().cpu()
+    ref = torch.nn.functional.scaled_dot_product_attention(q.float(), k[:, :, :661].float(), v[:, :, :661].float())
+    err = errors(ref.numpy(), got.numpy())
+    print(f"equal rows: snr={err['snr_db']:.1f} dB max_abs={err['max_abs']:.2e}", flush=True)
+    assert err["snr_db"] >= SNR_DB and err["max_abs"] <= MAX_ABS, err
+
+
+def test_single_valid_key_returns_v0_exactly(sidon):
+    """LK = 1: each query's one probability is exp2(0) = 1 and the others are
+    exactly 0, so every output row is v_0 bit for bit."""
+    q, k, v, rel = seeded_inputs(2, 3, 200, seed=55)
+    got = run(sidon, q, k, v, rel, [1, 1]).cpu()
+    assert torch.equal(got, v[:, :, :1, :].expand_as(got))
+
+
+def test_heads_are_independent(sidon):
+    """New inputs for one head leave every other head's output bit-identical."""
+    q, k, v, rel = seeded_inputs(1, 4, 300, seed=57)
+    a = run(sidon, q, k, v, rel, [271]).cpu()
+    gen = torch.Generator().manual_seed(58)
+    q2, k2, v2 = q.clone(), k.clone(), v.clone()
+    for t in (q2, k2, v2):
+        t[:, 2] = torch.randn(t[:, 2].shape, generator=gen).half()
+    b = run(sidon, q2, k2, v2, rel, [271]).cpu()
+    keep = [0, 1, 3]
+    assert torch.equal(a[:, keep], b[:, keep])
+    assert not torch.equal(a[:, 2], b[:, 2])
+
+
 def test_deterministic(sidon):
     q, k, v, rel = seeded_inputs(1, 16, 1000, seed=61)
     a = run(sidon, q, k, v, rel, [917])
