@@ -140,3 +140,108 @@ def test_gemm_rejects_bad_arguments_before_launch(sidon, over, code):
                                  args["ldy"], args["M"], args["N"], args["K"], args["act"], None)
     assert rc == code
     assert lib.sidon_last_error().decode()
+
+
+# The encoder and front-end entry points, the same way: fake aligned addresses
+# that are never dereferenced, each case wrong in exactly one argument, so
+# validation returns before any HIP call.  (No case is valid: on a GPU box a
+# valid call would launch a kernel on those addresses.)
+
+def _call(lib, name, base, over):
+    args = dict(base)
+    args.update(over)
+    rc = getattr(lib, name)(*args.values())
+    assert lib.sidon_last_error().decode(), name
+    return rc
+
+
+@pytest.mark.parametrize("over,code", [
+    (dict(x=None), -1),
+    (dict(n1_b=None), -1),
+    (dict(n2_w=None), -1),
+    (dict(xn=None), -1),
+    (dict(R=0), -2),
+    (dict(C=1022), -2),
+    (dict(C=4096), -2),
+    (dict(y=24), -4),
+    (dict(n1_w=8), -4),
+    (dict(xn=20), -4),
+    (dict(xn=24, xn_fp16=0), -4),
+])
+def test_res_norm_rejects_bad_arguments_before_launch(sidon, over, code):
+    base = dict(x=16, y=16, bias=16, n1_w=16, n1_b=16, eps1=1e-5, write_x=1, n2_w=16, n2_b=16, eps2=1e-5,
+                xn=16, xn_fp16=1, R=4800, C=1024, stream=None)
+    assert _call(sidon._lib.load(), "sidon_res_norm", base, over) == code
+
+
+@pytest.mark.parametrize("name,base,over,code", [
+    ("sidon_glu", dict(h=16, g=16, R=4800, C=1024, stream=None), dict(h=None), -1),
+    ("sidon_glu", dict(h=16, g=16, R=4800, C=1024, stream=None), dict(R=0), -2),
+    ("sidon_glu", dict(h=16, g=16, R=4800, C=1024, stream=None), dict(C=0), -2),
+    ("sidon_glu", dict(h=16, g=16, R=4800, C=1024, stream=None), dict(g=17), -4),
+    ("sidon_silu", dict(h=16, n=4800 * 4096, stream=None), dict(h=None), -1),
+    ("sidon_silu", dict(h=16, n=4800 * 4096, stream=None), dict(n=0), -2),
+    ("sidon_silu", dict(h=16, n=4800 * 4096, stream=None), dict(h=17), -4),
+])
+def test_elementwise_ops_reject_bad_arguments_before_launch(sidon, name, base, over, code):
+    assert _call(sidon._lib.load(), name, base, over) == code
+
+
+@pytest.mark.parametrize("over,code", [
+    (dict(src=None), -1),
+    (dict(dwt=None), -1),
+    (dict(out=None), -1),
+    (dict(B=0), -2),
+    (dict(T=0), -2),
+    (dict(C=1023), -2),
+    (dict(C=4096), -2),
+    (dict(K=5), -2),
+    (dict(src=18), -4),
+    (dict(ln_w=20), -4),
+])
+def test_causal_dw_norm_rejects_bad_arguments_before_launch(sidon, over, code):
+    base = dict(src=16, glu_input=1, dwt=16, ln_w=16, ln_b=16, eps=1e-5, out=16, B=1, T=4800, C=1024, K=31,
+                stream=None)
+    assert _call(sidon._lib.load(), "sidon_causal_dw_norm", base, over) == code
+
+
+FRAMES = dict(chunk=16, frames=16, B=1, S=1_536_000, stream=None)
+LOGMEL = dict(spec=16, mel_w=16, mel_lo=16, mel_len=16, max_len=30, logmel=16, R=9600, stream=None)
+
+
+@pytest.mark.parametrize("name,base,over,code", [
+    ("sidon_fbank_frames", FRAMES, dict(chunk=None), -1),
+    ("sidon_fbank_frames", FRAMES, dict(B=0), -2),
+    ("sidon_fbank_frames", FRAMES, dict(S=1000), -2),
+    ("sidon_fbank_frames", FRAMES, dict(S=160), -2),
+    ("sidon_fbank_frames", FRAMES, dict(frames=8), -4),
+    ("sidon_fbank_logmel", LOGMEL, dict(mel_lo=None), -1),
+    ("sidon_fbank_logmel", LOGMEL, dict(R=0), -2),
+    ("sidon_fbank_logmel", LOGMEL, dict(max_len=0), -2),
+    ("sidon_fbank_logmel", LOGMEL, dict(max_len=258), -2),
+])
+def test_fbank_entry_points_reject_bad_arguments_before_launch(sidon, name, base, over, code):
+    assert _call(sidon._lib.load(), name, base, over) == code
+
+
+def test_fbank_workspace_bytes(sidon):
+    lib = sidon._lib.load()
+    assert lib.sidon_fbank_workspace_bytes(0, 4800) == 0 and lib.sidon_fbank_workspace_bytes(1, 0) == 0
+    one = lib.sidon_fbank_workspace_bytes(1, 9600)
+    assert one > 0 and lib.sidon_fbank_workspace_bytes(3, 9600) == 3 * one
+    assert lib.sidon_fbank_workspace_bytes(1, 200) < one  # fewer statistics tiles for a short bucket
+
+
+@pytest.mark.parametrize("over,code", [
+    (dict(valid=None), -1),
+    (dict(B=0), -2),
+    (dict(F=0), -2),
+    (dict(F=9599), -2),
+    (dict(workspace_bytes=64), -2),
+    (dict(feats=32), -2),  # feats aliases logmel
+])
+def test_fbank_normalize_rejects_bad_arguments_before_launch(sidon, over, code):
+    lib = sidon._lib.load()
+    base = dict(logmel=32, valid=16, workspace=48, workspace_bytes=lib.sidon_fbank_workspace_bytes(1, 9600),
+                feats=64, B=1, F=9600, stream=None)
+    assert _call(lib, "sidon_fbank_normalize", base, over) == code
