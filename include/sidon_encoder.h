@@ -45,7 +45,7 @@ int sidon_glu(const void* h, void* g, int R, int C, sidon_stream_t stream);
 /*
  * In-place SiLU of n fp16 values: h = h * sigmoid(h), math in fp32.  Replaces
  * the in-place F.silu of the feed-forward modules
- * (src/sidon_triton/triton_encoder.py:485-486, :505-506).
+ * (src/sidon_triton/triton_encoder.py:498-499, :507-508).
  */
 int sidon_silu(void* h, int64_t n, sidon_stream_t stream);
 
@@ -58,8 +58,8 @@ int sidon_silu(void* h, int64_t n, sidon_stream_t stream);
  * fp32 sums, y [M, N] fp16 (row stride ldy); bias fp16 [N] or NULL.  SiLU
  * is taken in fp32 on the fp16-rounded sum and rounded to fp16, as
  * sidon_silu does after a separate GEMM.  Replaces the torch.addmm(b1, xn,
- * W1^T) + in-place F.silu pair of src/sidon_triton/triton_encoder.py:485-486
- * and :505-506.  Shapes: M >= 1, N a multiple of 256, K a multiple of 64;
+ * W1^T) + in-place F.silu pair of src/sidon_triton/triton_encoder.py:498-499
+ * and :507-508.  Shapes: M >= 1, N a multiple of 256, K a multiple of 64;
  * strides multiples of 8; x, w, y 16-byte aligned, bias 8-byte aligned.
  * sidon_gemm_bias_act_fits(M, N, K) says whether a shape is supported (pure
  * host function); sidon_gemm_bias_act_preferred(M, N, K) whether the kernel
@@ -72,6 +72,39 @@ int sidon_gemm_bias_act_preferred(int M, int N, int K);
 int sidon_gemm_bias_act(const void* x, int ldx, const void* w, int ldw, const void* bias, void* y, int ldy,
                         int M, int N, int K, int act, sidon_stream_t stream);
 
+/*
+ * Plain GEMM on rocBLAS with the kernel chosen per problem by timing:
+ *
+ *   y[m, n] = x[m, :] . w[n, :] + beta * y[m, n]      m < M, n < N, fp32 sums
+ *
+ * x [M, K] and w [N, K] row-major with row strides ldx, ldw >= K (K
+ * contiguous); y [M, N] row-major with row stride ldy >= N.  dtype 0: fp32
+ * x, w, y; 1: fp16 x, w, y (beta must be 0); 2: fp16 x, w and fp32 y.
+ * Used for the pointwise conv's first F.linear of the encoder
+ * (src/sidon_triton/triton_encoder.py:504; dtype 1) and the framing matmul
+ * of the front end (src/sidon_triton/frontend.py:222; dtype 0).  dtype 2
+ * with beta 1 is the form of the residual projections of res() (:491-492),
+ * which the encoder keeps on torch.addmm.
+ *
+ * sidon_gemm_nt runs the kernel recorded for the problem (shape, strides,
+ * dtype, beta != 0) by sidon_gemm_nt_tune, else rocBLAS's default.  The tuner
+ * times rocBLAS's default and every solution it lists for the problem, on
+ * scratch: y and y_check are two distinct buffers of y's shape and row stride
+ * (both overwritten; y's contents are the beta term while timing).  It
+ * records for the current device the fastest kernel whose product (beta = 0)
+ * agrees with the default's -- within 1e-5 relative for an fp32 output, 2e-3
+ * for fp16 -- and writes its solution index to *solution_out (INT_MIN: the
+ * default) when that is not NULL.  The tuner
+ * synchronises the stream and fails during stream capture; tune before
+ * capturing.  Every candidate is deterministic (rocBLAS atomics disabled).
+ * The first call on a device creates the device's rocBLAS handle, and
+ * rocBLAS sizes its workspace on first use of a problem: run each problem
+ * once outside capture.  Neither function has a counterpart in the reference.
+ */
+int sidon_gemm_nt(const void* x, int ldx, const void* w, int ldw, void* y, int ldy, int M, int N, int K, int dtype,
+                  float beta, sidon_stream_t stream);
+int sidon_gemm_nt_tune(const void* x, int ldx, const void* w, int ldw, void* y, void* y_check, int ldy, int M,
+                       int N, int K, int dtype, float beta, sidon_stream_t stream, int* solution_out);
 /*
  * Causal depthwise conv + LayerNorm + SiLU over B items of T frames:
  *

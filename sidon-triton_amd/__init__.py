@@ -13,6 +13,9 @@ Entry points (same argument meaning as the reference):
     attention (src/sidon_triton/triton_encoder.py:61-100, :491-503);
   * ``conformer.glu`` / ``conformer.causal_dw_norm`` / ``conformer.silu_`` --
     the conv module's and feed-forward's kernels (triton_encoder.py:113-181);
+  * ``blas.gemm_nt`` -- the encoder's and the front end's plain library GEMMs
+    on rocBLAS, kernel chosen per problem by timing (triton_encoder.py:491-492,
+    :504; frontend.py:222);
   * ``encoder.pack_encoder`` / ``encoder.HipEncoder`` / ``encoder.save_encoder``
     / ``encoder.load_encoder`` -- the whole 8-layer conformer encoder
     (triton_encoder.py:392-525);
@@ -28,8 +31,8 @@ The package directory name is not a Python identifier; the repository's
 entry scripts load it under the module name ``sidon_triton_amd``.
 """
 
-from . import (_lib, conformer, encoder, encoder_attention, encoder_block, flexrel, frontend, graphs, modeling,
-               runtime)
+from . import (_lib, blas, conformer, encoder, encoder_attention, encoder_block, flexrel, frontend, graphs,
+               modeling, runtime)
 from .flexrel import HEAD_DIM, LEFT, NUM_POS, RIGHT, flexrel_attention
 
 __all__ = [
@@ -37,6 +40,7 @@ __all__ = [
     "LEFT",
     "NUM_POS",
     "RIGHT",
+    "blas",
     "conformer",
     "encoder",
     "encoder_attention",

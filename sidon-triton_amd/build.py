@@ -17,7 +17,11 @@ from pathlib import Path
 PKG_DIR = Path(__file__).resolve().parent
 REPO_DIR = PKG_DIR.parent
 LIB_NAME = "libsidon_flexrel.so"
-SOURCES = [PKG_DIR / "csrc" / name for name in ("flexrel_fwd.hip", "res_norm.hip", "conformer_ops.hip", "fbank.hip", "gemm.hip")]
+SOURCES = [PKG_DIR / "csrc" / name
+           for name in ("flexrel_fwd.hip", "res_norm.hip", "conformer_ops.hip", "fbank.hip", "gemm.hip", "blas.hip")]
+# rocBLAS for the plain GEMMs of csrc/blas.hip.  Its soname is the one torch
+# bundles, so inside a torch process the library shares torch's copy.
+LIBS = ["-lrocblas"]
 ARCH = "gfx950"
 
 # -packed-fp32-ops: no v_pk_{add,mul,fma}_f32 in the generated code.
@@ -47,7 +51,7 @@ def build(verbose: bool = False) -> Path:
     """Compile the HIP library; returns its path.  Raises on a compile error."""
     out = PKG_DIR / LIB_NAME
     tmp = out.with_name(out.name + f".tmp{os.getpid()}")
-    cmd = [hipcc(), *HIP_FLAGS, f"-I{REPO_DIR / 'include'}", "-o", str(tmp), *map(str, SOURCES)]
+    cmd = [hipcc(), *HIP_FLAGS, f"-I{REPO_DIR / 'include'}", "-o", str(tmp), *map(str, SOURCES), *LIBS]
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)

@@ -5,7 +5,7 @@ Same names and argument meaning as src/sidon_triton/triton_encoder.py:
   * ``glu(h)`` (:127-133): h [R, 2C] fp16 -> h[:, :C] * sigmoid(h[:, C:]) fp16;
   * ``causal_dw_norm(g, batch, dwt, ln_w, ln_b, eps)`` (:163-181): g [B*T, C]
     fp16, dwt [K, C] fp32 -> silu(LN(causal depthwise conv)) fp16;
-  * ``silu_(h)``: the in-place F.silu of the feed-forward modules (:485-486);
+  * ``silu_(h)``: the in-place F.silu of the feed-forward modules (:498-499);
   * ``linear_silu(x, w, b)``: the feed-forward input projection and that SiLU
     in one kernel (``silu_(torch.addmm(b, x, w.t()))`` up to the GEMM's
     summation order; csrc/gemm.hip), for the shapes ``linear_silu_fits``

@@ -7,7 +7,7 @@
 //
 // They replace _glu_kernel / glu and _causal_dw_norm_kernel / causal_dw_norm
 // of src/sidon_triton/triton_encoder.py:113-181, and the in-place F.silu of
-// the feed-forward modules (:485-486, :505-506).  causal_dw_norm can also read
+// the feed-forward modules (:498-499, :507-508).  causal_dw_norm can also read
 // the pointwise conv's output h [R, 2C] and form g = GLU(h) on the fly (g is
 // rounded to fp16 exactly as glu stores it), which saves the g round trip
 // through HBM.

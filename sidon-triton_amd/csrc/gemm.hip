@@ -6,7 +6,7 @@
 // X [M, K] and W [N, K] fp16 (both K-contiguous: activations and a torch
 // Linear weight), fp32 accumulation, Y [M, N] fp16.  This is the
 // torch.addmm(b1, xn, W1^T) + F.silu_ pair of the FFN modules of
-// src/sidon_triton/triton_encoder.py:485-486 and :505-506, in one pass: the
+// src/sidon_triton/triton_encoder.py:498-499 and :507-508, in one pass: the
 // bias is added to the fp32 sum and rounded to fp16 (as the addmm stores it),
 // then SiLU is taken in fp32 and rounded to fp16 (as the in-place SiLU does),
 // so the only difference from the two-step form is the GEMM's summation order.

@@ -33,6 +33,7 @@ from pathlib import Path
 
 import torch
 
+from .blas import gemm_nt
 from .conformer import glu_causal_dw_norm, linear_silu, linear_silu_preferred, silu_
 from .encoder_attention import flexrel_attention
 from .encoder_block import res_norm
@@ -228,6 +229,9 @@ class HipEncoder:
             return silu_(torch.addmm(b, xn, w.t(), out=h_buf))
 
         def res(a, w, bias, **kw):
+            # The residual projections stay on torch.addmm (hipBLASLt): inside
+            # the encoder graph rocBLAS's timed choice was no faster for the
+            # feed-forward output and slower for the hid -> hid projections.
             torch.addmm(x, a, w.t(), out_dtype=torch.float32, out=x)
             return res_norm(x, bias=bias, xn=xn_buf if kw.get("norm2") is not None else None, **kw)
 
@@ -239,7 +243,7 @@ class HipEncoder:
             qkv = torch.addmm(p["qkv_b"], xn, p["qkv_w"].t(), out=qkv_buf)
             c = flexrel_attention(qkv, batch, self.heads, p["rel"], lens, out=ctx)
             xn = res(c, p["out_w"], b2, norm2=p["conv_ln"], write_x=False)
-            pw1 = torch.mm(xn, p["pw1_w"].t(), out=pw1_buf)
+            pw1 = gemm_nt(xn, p["pw1_w"], pw1_buf)
             s = glu_causal_dw_norm(pw1, batch, p["dwt"], *p["dw_ln"], out=ctx)
             xn = res(s, p["pw2_w"], b2, norm2=p["ffn2_ln"], write_x=False)
             h = ffn_in(p["ffn2_w1"], p["ffn2_b1"])

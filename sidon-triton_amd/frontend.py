@@ -29,6 +29,7 @@ import numpy as np
 import torch
 
 from . import _lib
+from .blas import gemm_nt
 from .flexrel import _check_device_tensor, _stream_handle
 
 SAMPLE_RATE = 16_000
@@ -172,7 +173,7 @@ class Fbank:
             rc = lib.sidon_fbank_frames(chunk.data_ptr(), fr.data_ptr(), batch, samples, stream)
         _lib.check("sidon_fbank_frames", rc)
         spec = ws["spec"][:batch * frames * 2 * N_BINS].view(batch * frames, 2 * N_BINS)
-        torch.mm(fr, self.weight_t.t(), out=spec)
+        gemm_nt(fr, self.weight_t, spec)
         logmel = ws["logmel"][:batch * frames * NUM_MEL]
         if out is None:
             out = torch.empty(batch, frames // 2, 2 * NUM_MEL, device=device)

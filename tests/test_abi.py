@@ -245,3 +245,28 @@ def test_fbank_normalize_rejects_bad_arguments_before_launch(sidon, over, code):
     base = dict(logmel=32, valid=16, workspace=48, workspace_bytes=lib.sidon_fbank_workspace_bytes(1, 9600),
                 feats=64, B=1, F=9600, stream=None)
     assert _call(lib, "sidon_fbank_normalize", base, over) == code
+
+
+@pytest.mark.parametrize("over,code", [
+    (dict(x=None), -1),
+    (dict(y=None), -1),
+    (dict(M=0), -2),
+    (dict(K=0), -2),
+    (dict(dtype=3), -2),
+    (dict(dtype=1, beta=1.0), -2),  # an fp16 output takes beta = 0 only
+    (dict(M=1 << 20, ldx=4096), -2),  # 2^32 elements
+    (dict(ldx=1000), -3),
+    (dict(ldw=1000), -3),
+    (dict(ldy=1000), -3),
+    (dict(dtype=0, beta=0.0, x=18), -4),  # fp32 operands: 4-byte alignment
+    (dict(dtype=1, beta=0.0, w=17), -4),
+    (dict(dtype=0, beta=0.0, y=18), -4),  # fp32 output
+])
+def test_gemm_nt_rejects_bad_arguments_before_launch(sidon, over, code):
+    base = dict(x=16, ldx=4096, w=16, ldw=4096, y=16, ldy=1024, M=4800, N=1024, K=4096, dtype=2, beta=1.0,
+                stream=None)
+    lib = sidon._lib.load()
+    assert _call(lib, "sidon_gemm_nt", base, over) == code
+    tune_base = dict(x=base["x"], ldx=base["ldx"], w=base["w"], ldw=base["ldw"], y=base["y"], y_check=32,
+                     **{k: base[k] for k in ("ldy", "M", "N", "K", "dtype", "beta", "stream")}, solution_out=None)
+    assert _call(lib, "sidon_gemm_nt_tune", tune_base, over) == code

@@ -1,0 +1,129 @@
+"""The rocBLAS-backed plain GEMMs (csrc/blas.hip, ``blas.gemm_nt``) against a
+float64 reference, tuned and untuned, and under HIP graph capture (needs an
+MI355X).
+
+Bar: fp32 sums, so an fp32 output is within 2e-6 relative (Frobenius) of the
+float64 product and an fp16 output within fp16 rounding (2e-3); a tuned
+problem and repeated calls are bit-identical (every candidate kernel is
+deterministic)."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+TOL = {torch.float32: 2e-6, torch.float16: 2e-3}
+
+
+def _problem(m, n, k, in_dtype, out_dtype, seed, ldx=None, ldy=None):
+    gen = torch.Generator().manual_seed(seed)
+    ldx = k if ldx is None else ldx
+    ldy = n if ldy is None else ldy
+    x = torch.randn(m, ldx, generator=gen).to(in_dtype).to(DEV)[:, :k]
+    w = (torch.randn(n, k, generator=gen) / k ** 0.5).to(in_dtype).to(DEV)
+    y0 = torch.randn(m, ldy, generator=gen).to(out_dtype).to(DEV)[:, :n]
+    return x, w, y0
+
+
+def _reference(x, w, y0, beta):
+    return x.double().cpu() @ w.double().cpu().t() + beta * y0.double().cpu()
+
+
+def _rel(got, ref):
+    got = got.double().cpu()
+    return float((got - ref).norm() / ref.norm())
+
+
+@pytest.mark.parametrize("m,n,k,in_dtype,out_dtype,beta,ldx,ldy", [
+    (9600, 514, 400, torch.float32, torch.float32, 0.0, None, None),      # framing GEMM
+    (4800, 2048, 1024, torch.float16, torch.float16, 0.0, None, None),    # pointwise conv 1
+    (4800, 1024, 4096, torch.float16, torch.float32, 1.0, None, None),    # FFN output into the stream
+    (4800, 1024, 1024, torch.float16, torch.float32, 1.0, None, None),    # out-projection / pointwise conv 2
+    (333, 100, 70, torch.float32, torch.float32, 0.5, 80, 130),           # odd sizes, strided views
+    (1, 7, 3, torch.float16, torch.float32, 1.0, None, None),
+    (77, 130, 96, torch.float16, torch.float16, 0.0, 128, 136),
+])
+def test_gemm_nt_matches_float64(sidon, m, n, k, in_dtype, out_dtype, beta, ldx, ldy):
+    x, w, y0 = _problem(m, n, k, in_dtype, out_dtype, seed=m + n + k, ldx=ldx, ldy=ldy)
+    ref = _reference(x, w, y0, beta)
+    out = y0.clone() if ldy is None else torch.empty(m, ldy, dtype=out_dtype, device=DEV)[:, :n].copy_(y0)
+    sidon.blas.gemm_nt(x, w, out, beta=beta)  # first call: tuned, then run
+    torch.cuda.synchronize()
+    err = _rel(out, ref)
+    print(f"M={m} N={n} K={k} {in_dtype}->{out_dtype} beta={beta}: rel err {err:.2e}", flush=True)
+    assert err <= TOL[out_dtype], err
+    again = y0.clone() if ldy is None else torch.empty(m, ldy, dtype=out_dtype, device=DEV)[:, :n].copy_(y0)
+    sidon.blas.gemm_nt(x, w, again, beta=beta)  # the recorded kernel
+    torch.cuda.synchronize()
+    assert torch.equal(out, again)
+
+
+def test_gemm_nt_untuned_default_matches_float64(sidon, monkeypatch):
+    """rocBLAS's default kernel (tuning switched off) meets the same bar."""
+    monkeypatch.setenv("SIDON_GEMM_TUNE", "0")
+    x, w, y0 = _problem(1234, 1024, 1024, torch.float16, torch.float32, seed=3)
+    out = y0.clone()
+    sidon.blas.gemm_nt(x, w, out, beta=1.0)
+    torch.cuda.synchronize()
+    assert _rel(out, _reference(x, w, y0, 1.0)) <= TOL[torch.float32]
+
+
+def test_gemm_nt_graph_replays_match_eager(sidon):
+    """Two accumulating GEMMs captured into a HIP graph and replayed three
+    times from the same start, with eager work and synchronisations between
+    the replays: every replay equals the eager sequence bit for bit."""
+    x, w, y0 = _problem(4800, 1024, 4096, torch.float16, torch.float32, seed=11)
+    x2, w2, _ = _problem(4800, 1024, 1024, torch.float16, torch.float32, seed=12)
+    y = y0.clone()
+
+    def enqueue():
+        sidon.blas.gemm_nt(x, w, y, beta=1.0)
+        sidon.blas.gemm_nt(x2, w2, y, beta=1.0)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        enqueue()  # eager warm-up: tunes both problems
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    y.copy_(y0)
+    enqueue()
+    torch.cuda.synchronize()
+    eager = y.clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        enqueue()
+    for rep in range(3):
+        y.copy_(y0)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, eager), rep
+        _ = (x2.float() * 2).sum().item()  # unrelated eager work
+
+
+def test_tuner_refuses_to_run_during_capture(sidon):
+    """The tuner times kernels with host synchronisation, which capture
+    forbids: it returns an error instead (the wrapper never calls it then)."""
+    import ctypes
+
+    lib = sidon._lib.load()
+    x, w, y0 = _problem(64, 64, 64, torch.float16, torch.float16, seed=5)
+    y = y0.clone()
+    sidon.blas.gemm_nt(x, w, y)  # outside capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    rc, msg = None, ""
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph):
+            rc = lib.sidon_gemm_nt_tune(x.data_ptr(), 64, w.data_ptr(), 64, y.data_ptr(), y0.data_ptr(), 64, 64, 64,
+                                        64, 1, 0.0, torch.cuda.current_stream().cuda_stream,
+                                        ctypes.byref(ctypes.c_int()))
+            msg = lib.sidon_last_error().decode()
+            sidon.blas.gemm_nt(x, w, y)  # a captured run of the recorded kernel
+    assert rc == -5 and "capture" in msg, (rc, msg)
+    graph.replay()
+    torch.cuda.synchronize()
