@@ -9,8 +9,9 @@
 //              count of true frames is 1.0; later frames 0.  [B, F, 80] is
 //              also the stride-2 stacked [B, F / 2, 160] layout.
 //
-// logmel: one wavefront per frame; the 257 powers go to LDS, then lane m sums
-// the nonzero span of mel triangle m (sparse: start bin, length, weights).
+// logmel: 12 frames per block; their 257 powers go to LDS, then thread
+// (m, lane) sums the nonzero span of mel triangle m (sparse: start bin,
+// length, weights) for 4 of the frames, loading each weight once.
 // normalize: statistics are per-tile two-pass sums (fixed tiles of frames,
 // one block per (tile, item)), merged by a fixed pairwise tree, one block per (bin group, item) --
 // deterministic, no atomics -- through a caller-provided workspace; a third
@@ -36,7 +37,9 @@ constexpr int kEdgePad = 160;
 constexpr float kMelFloor = 1.192092955078125e-07f;
 constexpr float kVarEps = 1e-7f;
 constexpr float kPadValue = 1.0f;
-constexpr int kFramesPerBlock = 4;   // logmel: one wavefront each
+constexpr int kLmFrames = 12;        // logmel: frames per block
+constexpr int kLmLanes = 3;          // logmel: threads per mel bin (each kLmFrames / kLmLanes frames)
+constexpr int kLmThreads = 256;      // logmel: threads per block (kMel * kLmLanes = 240 sum)
 constexpr int kLanes = 4;            // normalize: frame lanes x 80 bins per block
 constexpr int kApplyFrames = 64;     // normalize: frames per apply block
 constexpr int kMaxTiles = 64;
@@ -70,44 +73,58 @@ __global__ void __launch_bounds__(256) frames_kernel(const float* __restrict__ c
   *reinterpret_cast<float4*>(frames + e) = v;
 }
 
-__global__ void __launch_bounds__(64 * kFramesPerBlock) logmel_kernel(const float* __restrict__ spec,
-                                                                     const float* __restrict__ mel_w,
-                                                                     const int* __restrict__ mel_lo,
-                                                                     const int* __restrict__ mel_len, int max_len,
-                                                                     float* __restrict__ out, int R) {
-  __shared__ float power[kFramesPerBlock][kBins + 3];
-  const int lane = threadIdx.x & 63;
-  const int w = threadIdx.x >> 6;
-  const int r = blockIdx.x * kFramesPerBlock + w;
-  if (r < R) {
-    // All of the lane's loads in flight together (unrolled, guarded).
-    const float* row = spec + (int64_t)r * kSpecWidth;
-    constexpr int kPer = (kBins + 63) / 64;
+__global__ void __launch_bounds__(kLmThreads) logmel_kernel(const float* __restrict__ spec,
+                                                          const float* __restrict__ mel_w,
+                                                          const int* __restrict__ mel_lo,
+                                                          const int* __restrict__ mel_len, int max_len,
+                                                          float* __restrict__ out, int R) {
+  __shared__ float power[kLmFrames][kBins + 3];
+  const int f0 = blockIdx.x * kLmFrames;
+  // Power spectra of the block's frames, every load of a thread in flight
+  // together (consecutive threads read consecutive bins of a frame).
+  {
+    constexpr int kPer = (kLmFrames * kBins + kLmThreads - 1) / kLmThreads;
     float re[kPer], im[kPer];
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {
-      const int k = lane + 64 * j;
-      re[j] = k < kBins ? row[k] : 0.f;
-      im[j] = k < kBins ? row[kBins + k] : 0.f;
+      const int idx = threadIdx.x + kLmThreads * j;
+      const int f = idx / kBins;
+      const int k = idx - f * kBins;
+      const bool ok = idx < kLmFrames * kBins && f0 + f < R;
+      const float* row = spec + (int64_t)(f0 + f) * kSpecWidth;
+      re[j] = ok ? row[k] : 0.f;
+      im[j] = ok ? row[kBins + k] : 0.f;
     }
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {
-      const int k = lane + 64 * j;
-      if (k < kBins) power[w][k] = re[j] * re[j] + im[j] * im[j];
+      const int idx = threadIdx.x + kLmThreads * j;
+      const int f = idx / kBins;
+      if (idx < kLmFrames * kBins) power[f][idx - f * kBins] = re[j] * re[j] + im[j] * im[j];
     }
   }
   __syncthreads();
-  if (r >= R) return;
-  for (int m = lane; m < kMel; m += 64) {
-    const int lo = mel_lo[m];
-    const int n = mel_len[m];
-    const float* wm = mel_w + m * max_len;
-    float acc = 0.f;
-    // (unrolled so that several weight loads are in flight; the sum keeps
-    // its order i = 0 .. n - 1)
-#pragma unroll 8
-    for (int i = 0; i < n; ++i) acc = fmaf(wm[i], power[w][lo + i], acc);
-    out[(int64_t)r * kMel + m] = logf(fmaxf(acc, kMelFloor));
+  // Thread (mel m, lane fl) sums frames fl, fl + kLmLanes, ...: each weight
+  // is loaded once for kLmFrames / kLmLanes frames.  Every sum keeps the
+  // order i = 0 .. n - 1.
+  const int t = threadIdx.x;
+  if (t >= kMel * kLmLanes) return;
+  const int m = t % kMel;
+  const int fl = t / kMel;
+  const int lo = mel_lo[m];
+  const int n = mel_len[m];
+  const float* wm = mel_w + m * max_len;
+  constexpr int kPerLane = kLmFrames / kLmLanes;
+  float acc[kPerLane] = {};
+#pragma unroll 4
+  for (int i = 0; i < n; ++i) {
+    const float wv = wm[i];
+#pragma unroll
+    for (int j = 0; j < kPerLane; ++j) acc[j] = fmaf(wv, power[fl + kLmLanes * j][lo + i], acc[j]);
+  }
+#pragma unroll
+  for (int j = 0; j < kPerLane; ++j) {
+    const int r = f0 + fl + kLmLanes * j;
+    if (r < R) out[(int64_t)r * kMel + m] = logf(fmaxf(acc[j], kMelFloor));
   }
 }
 
@@ -296,8 +313,8 @@ SIDON_API int sidon_fbank_logmel(const float* spec, const float* mel_w, const in
   int rc;
   if ((rc = sidon::check_device())) return rc;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(logmel_kernel, dim3((unsigned)((R + kFramesPerBlock - 1) / kFramesPerBlock)),
-                     dim3(64 * kFramesPerBlock), 0, s, spec, mel_w, mel_lo, mel_len, max_len, logmel, R);
+  hipLaunchKernelGGL(logmel_kernel, dim3((unsigned)((R + kLmFrames - 1) / kLmFrames)), dim3(kLmThreads), 0, s, spec,
+                     mel_w, mel_lo, mel_len, max_len, logmel, R);
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) return fail(SIDON_E_LAUNCH, "fbank logmel launch failed: %s", hipGetErrorString(err));
   return SIDON_OK;
