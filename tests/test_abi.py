@@ -270,3 +270,35 @@ def test_gemm_nt_rejects_bad_arguments_before_launch(sidon, over, code):
     tune_base = dict(x=base["x"], ldx=base["ldx"], w=base["w"], ldw=base["ldw"], y=base["y"], y_check=32,
                      **{k: base[k] for k in ("ldy", "M", "N", "K", "dtype", "beta", "stream")}, solution_out=None)
     assert _call(lib, "sidon_gemm_nt_tune", tune_base, over) == code
+
+
+def test_gemm_nt_wrapper_rejects_bad_tensors(sidon):
+    """blas.gemm_nt checks devices, types and shapes in Python, before any
+    library call (host tensors never reach the C ABI)."""
+    import torch
+
+    x = torch.zeros(8, 16)
+    w = torch.zeros(4, 16)
+    out = torch.zeros(8, 4)
+    with pytest.raises(ValueError, match="HIP device"):
+        sidon.blas.gemm_nt(x, w, out)
+    # type and shape checks run after the device check, so drive them with a
+    # tensor subclass that reports a HIP device without holding device memory
+    class FakeDev(torch.Tensor):
+        @property
+        def device(self):
+            return torch.device("cuda:0")
+
+    def fake(t):
+        return t.as_subclass(FakeDev)
+
+    with pytest.raises(ValueError, match="x is"):
+        sidon.blas.gemm_nt(fake(x), fake(w.half()), fake(out))
+    with pytest.raises(ValueError, match="unsupported types"):
+        sidon.blas.gemm_nt(fake(x), fake(w), fake(out.half()))
+    with pytest.raises(ValueError, match="beta = 0"):
+        sidon.blas.gemm_nt(fake(x.half()), fake(w.half()), fake(out.half()), beta=1.0)
+    with pytest.raises(ValueError, match="do not match"):
+        sidon.blas.gemm_nt(fake(x), fake(torch.zeros(4, 15)), fake(out))
+    with pytest.raises(ValueError, match="contiguous rows"):
+        sidon.blas.gemm_nt(fake(x.t()), fake(w), fake(out))
