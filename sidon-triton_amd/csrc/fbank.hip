@@ -50,17 +50,18 @@ constexpr int kMergeThreads = 320;   // merge: threads per block (32 tile pairs 
 // frames[b, f, i] = chunk[b, 160 f + i - 160] (zero outside [0, S)): the
 // (160, 160) edge padding and the 400 / 160 framing in one pass, 4 samples
 // per thread.
+// Block (x, item b): 256 of the item's F * 100 16-byte frame chunks; 32-bit
+// index math within the item (F * 100 < 2^32; the division by 100 is a
+// multiply).
 __global__ void __launch_bounds__(256) frames_kernel(const float* __restrict__ chunk, float* __restrict__ frames,
-                                                    int S, int F, int64_t total4, bool vec4) {
-  const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (q >= total4) return;
-  const int64_t e = q * 4;                       // element of [B, F, 400]
-  const int64_t row = e / kFrameSize;            // b * F + f
-  const int i = (int)(e - row * kFrameSize);     // 0, 4, ..., 396
-  const int64_t b = row / F;
-  const int f = (int)(row - b * F);
-  const int t0 = f * kFrameShift + i - kEdgePad;
-  const float* src = chunk + b * S;
+                                                    int S, int F, bool vec4) {
+  constexpr uint32_t kPerRow = kFrameSize / 4;  // 100 chunks of 4 samples
+  const uint32_t q = blockIdx.x * 256u + threadIdx.x;
+  if (q >= (uint32_t)F * kPerRow) return;
+  const uint32_t f = q / kPerRow;
+  const int i = (int)(q - f * kPerRow) * 4;     // 0, 4, ..., 396
+  const int t0 = (int)f * kFrameShift + i - kEdgePad;
+  const float* src = chunk + (int64_t)blockIdx.y * S;
   float4 v;
   if (t0 >= 0 && t0 + 3 < S && vec4) {
     v = *reinterpret_cast<const float4*>(src + t0);  // t0 % 4 == 0; rows 16-byte aligned
@@ -70,7 +71,7 @@ __global__ void __launch_bounds__(256) frames_kernel(const float* __restrict__ c
     v.z = (t0 + 2 >= 0 && t0 + 2 < S) ? src[t0 + 2] : 0.f;
     v.w = (t0 + 3 >= 0 && t0 + 3 < S) ? src[t0 + 3] : 0.f;
   }
-  *reinterpret_cast<float4*>(frames + e) = v;
+  *reinterpret_cast<float4*>(frames + ((int64_t)blockIdx.y * F + f) * kFrameSize + i) = v;
 }
 
 __global__ void __launch_bounds__(kLmThreads) logmel_kernel(const float* __restrict__ spec,
@@ -330,12 +331,15 @@ SIDON_API int sidon_fbank_frames(const float* chunk, float* frames, int B, int S
   int rc;
   if ((rc = sidon::check_device())) return rc;
   const int F = S / kFrameShift;
-  const int64_t total4 = (int64_t)B * F * kFrameSize / 4;
   // 16-byte source loads when every item's row starts 16-byte aligned (S is a
   // multiple of 320, so that holds when the chunk pointer is aligned).
   const bool vec4 = sidon::aligned16(chunk);
-  hipLaunchKernelGGL(frames_kernel, dim3((unsigned)((total4 + 255) / 256)), dim3(256), 0,
-                     reinterpret_cast<hipStream_t>(stream), chunk, frames, S, F, total4, vec4);
+  const unsigned blocks = (unsigned)(((int64_t)F * (kFrameSize / 4) + 255) / 256);
+  for (int b0 = 0; b0 < B; b0 += 65535) {  // items on grid y, at most 65535 per launch
+    const int nb = B - b0 < 65535 ? B - b0 : 65535;
+    hipLaunchKernelGGL(frames_kernel, dim3(blocks, (unsigned)nb), dim3(256), 0, reinterpret_cast<hipStream_t>(stream),
+                       chunk + (int64_t)b0 * S, frames + (int64_t)b0 * F * kFrameSize, S, F, vec4);
+  }
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) return fail(SIDON_E_LAUNCH, "fbank frames launch failed: %s", hipGetErrorString(err));
   return SIDON_OK;
