@@ -302,3 +302,15 @@ def test_gemm_nt_wrapper_rejects_bad_tensors(sidon):
         sidon.blas.gemm_nt(fake(x), fake(torch.zeros(4, 15)), fake(out))
     with pytest.raises(ValueError, match="contiguous rows"):
         sidon.blas.gemm_nt(fake(x.t()), fake(w), fake(out))
+
+
+def test_build_compiles_every_source_file():
+    """build.py's source list is exactly csrc/*.hip, so a new kernel file
+    cannot be left out of the library (its symbols would be missing at
+    load time, not at build time)."""
+    import importlib.util
+
+    spec = importlib.util.spec_from_file_location("sidon_build", ROOT / "sidon-triton_amd" / "build.py")
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    assert sorted(p.name for p in mod.SOURCES) == sorted(p.name for p in (ROOT / "sidon-triton_amd" / "csrc").glob("*.hip"))
