@@ -35,6 +35,14 @@ Pinning (what checks each function, see tests/test_oracle.py):
   * ``torch_core_chunked``: equals ``flexrel_reference`` to fp32 rounding.
   * ``flexrel_bruteforce``: scalar loops with ``math.exp`` -- an independent
     statement, checked against the transformers golden vectors.
+  * ``errors``: closed-form known answers (a constant reference scaled by
+    1 + eps gives relative RMSE eps and SNR -20 log10 eps, exactly 60 dB at
+    1e-3; a +-1 reference plus delta; an uneven two-element case whose RMS,
+    mean |delta| and rms(actual) all differ; identical inputs hit the 1e-12
+    noise floor), with planted variants (mean |delta|, 10 log10, signal from
+    ``actual``) that the known answers reject.
+  * ``attention_flops``: the 95.09 / 2.416 GFLOP figures of the c3 / c1
+    configurations.
 Planted-mistake tests mutate this module's formula (sign of the distance,
 clamp bounds, scale placement, mask) and require the golden check to fail.
 
@@ -259,17 +267,32 @@ def torch_core_chunked(q, k, v, rel, lens=None, out=None, chunk: int = 512, dtyp
     return out
 
 
-def errors(reference, actual) -> dict:
-    """max_abs / relative RMSE / SNR dB as in src/sidon_triton/engines.py:47-55."""
+def errors(reference, actual, *, _noise: str = "rms", _db_factor: float = 20.0,
+           _signal_from: str = "reference") -> dict:
+    """max_abs / relative RMSE / SNR dB as in src/sidon_triton/engines.py:47-55.
+
+    signal = rms(reference), noise = rms(reference - actual) (the noise floor
+    is clamped at 1e-12 as there; here also the signal at 1e-30, so an
+    all-zero reference gives a finite, very negative SNR instead of a math
+    error), snr_db = 20 log10(signal / noise).  Evaluated in float64.
+
+    The underscored keywords exist only so tests can plant mistakes (mean
+    |delta| instead of the RMS, a 10 log10 power ratio, the signal taken from
+    ``actual``) and show that the closed-form known answers reject them.
+    """
     ref = np.asarray(reference, dtype=np.float64)
     act = np.asarray(actual, dtype=np.float64)
     delta = np.abs(ref - act)
-    signal = math.sqrt(float(np.mean(ref * ref))) if ref.size else 0.0
-    noise = math.sqrt(float(np.mean(delta * delta))) if ref.size else 0.0
+    sig_src = ref if _signal_from == "reference" else act
+    signal = math.sqrt(float(np.mean(sig_src * sig_src))) if ref.size else 0.0
+    if _noise == "rms":
+        noise = math.sqrt(float(np.mean(delta * delta))) if ref.size else 0.0
+    else:
+        noise = float(np.mean(delta)) if ref.size else 0.0
     return {
         "max_abs": float(delta.max()) if delta.size else 0.0,
         "relative_rmse": noise / max(signal, 1e-12),
-        "snr_db": 20.0 * math.log10(max(signal, 1e-30) / max(noise, 1e-12)),
+        "snr_db": _db_factor * math.log10(max(signal, 1e-30) / max(noise, 1e-12)),
     }
 
 

@@ -158,3 +158,77 @@ def test_flop_count():
     # BASELINE: 95.09 GFLOP per L=4800, H=16 layer
     assert math.isclose(attention_flops(16, 4800, 4800) / 1e9, 95.09, rel_tol=1e-3)
     assert math.isclose(attention_flops(16, 750, 750) / 1e9, 2.416, rel_tol=1e-3)
+
+
+# ---- errors(): the SNR / relative RMSE / max |err| judge of every parity test
+# (src/sidon_triton/engines.py:47-55), pinned by closed-form known answers.
+
+def _known_answer_cases():
+    """(reference, actual, expected max_abs, relative_rmse, snr_db)."""
+    cases = []
+    # constant reference c, actual = c (1 + eps): noise = c eps everywhere
+    for c, eps in ((2.5, 1e-3), (0.75, 3e-4), (10.0, 0.05)):
+        ref = np.full((3, 7, 11), c)
+        cases.append((ref, ref * (1.0 + eps), c * eps, eps, -20.0 * math.log10(eps)))
+    # reference +-1, actual = reference + delta: signal 1, noise |delta|
+    rng = np.random.default_rng(5)
+    for delta in (1e-3, 2e-2, -4e-4):
+        ref = rng.choice([-1.0, 1.0], size=(64, 64))
+        cases.append((ref, ref + delta, abs(delta), abs(delta), -20.0 * math.log10(abs(delta))))
+    # uneven error: ref (3, 4), error (0, 1): rms(ref) = sqrt(12.5),
+    # rms(err) = sqrt(0.5) -> relative RMSE exactly 0.2, SNR 20 log10(5);
+    # mean |err| (0.5), rms(actual) = sqrt(17) and 10 log10 all differ
+    cases.append((np.array([3.0, 4.0]), np.array([3.0, 5.0]), 1.0, 0.2, 20.0 * math.log10(5.0)))
+    return cases
+
+
+@pytest.mark.parametrize("case", range(7))
+def test_errors_known_answers(case):
+    ref, act, max_abs, rel, snr = _known_answer_cases()[case]
+    got = errors(ref, act)
+    assert math.isclose(got["max_abs"], max_abs, rel_tol=1e-9)
+    assert math.isclose(got["relative_rmse"], rel, rel_tol=1e-9)
+    assert math.isclose(got["snr_db"], snr, rel_tol=1e-9)
+    # symmetric inputs in torch / fp32 arrays give the same numbers
+    got32 = errors(torch.from_numpy(ref.astype(np.float32)), act.astype(np.float32))
+    assert math.isclose(got32["snr_db"], snr, abs_tol=1e-3)
+
+
+def test_errors_sixty_db_at_one_part_in_a_thousand():
+    # the north-star bar: relative error 1e-3 is exactly 60 dB
+    ref = np.full(1000, 1.7)
+    assert math.isclose(errors(ref, ref * 1.001)["snr_db"], 60.0, rel_tol=1e-9)
+    assert errors(ref, ref * 1.0011)["snr_db"] < 60.0 < errors(ref, ref * 1.0009)["snr_db"]
+
+
+def test_errors_identical_inputs_hit_the_noise_floor():
+    ref = np.array([[1.0, -1.0], [1.0, -1.0]])
+    got = errors(ref, ref.copy())
+    assert got["max_abs"] == 0.0 and got["relative_rmse"] == 0.0
+    # noise clamped at 1e-12: 20 log10(1 / 1e-12) = 240 dB
+    assert math.isclose(got["snr_db"], 240.0, rel_tol=1e-12)
+    assert errors(np.zeros(4), np.zeros(4))["snr_db"] < -300.0  # zero signal, no math error
+
+
+def test_errors_max_abs_is_the_largest_elementwise_difference():
+    ref = np.zeros((5, 5))
+    act = ref.copy()
+    act[3, 1] = -0.25
+    act[0, 4] = 0.125
+    got = errors(ref, act)
+    assert got["max_abs"] == 0.25
+    # signal 0: relative RMSE = noise / 1e-12
+    assert math.isclose(got["relative_rmse"], math.sqrt((0.25**2 + 0.125**2) / 25) / 1e-12, rel_tol=1e-12)
+
+
+@pytest.mark.parametrize("mutation", [dict(_noise="mean_abs"), dict(_db_factor=10.0),
+                                      dict(_signal_from="actual")])
+def test_errors_planted_mistakes_are_caught(mutation):
+    # every mutation fails at least one known answer
+    failed = 0
+    for ref, act, max_abs, rel, snr in _known_answer_cases():
+        got = errors(ref, act, **mutation)
+        ok = (math.isclose(got["relative_rmse"], rel, rel_tol=1e-6)
+              and math.isclose(got["snr_db"], snr, rel_tol=1e-6))
+        failed += not ok
+    assert failed > 0, mutation
