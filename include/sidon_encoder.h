@@ -87,24 +87,41 @@ int sidon_gemm_bias_act(const void* x, int ldx, const void* w, int ldw, const vo
  * which the encoder keeps on torch.addmm.
  *
  * sidon_gemm_nt runs the kernel recorded for the problem (shape, strides,
- * dtype, beta != 0) by sidon_gemm_nt_tune, else rocBLAS's default.  The tuner
- * times rocBLAS's default and every solution it lists for the problem, on
- * scratch: y and y_check are two distinct buffers of y's shape and row stride
- * (both overwritten; y's contents are the beta term while timing).  It
- * records for the current device the fastest kernel whose product (beta = 0)
- * agrees with the default's -- within 1e-5 relative for an fp32 output, 2e-3
- * for fp16 -- and writes its solution index to *solution_out (INT_MIN: the
- * default) when that is not NULL.  The tuner
+ * dtype, beta != 0) by sidon_gemm_nt_tune or sidon_gemm_nt_pin, else
+ * rocBLAS's default.  The tuner times rocBLAS's default and every solution
+ * it lists for the problem that needs no workspace (rocBLAS's device-memory
+ * size query), on scratch: y and y_check are two distinct buffers of y's
+ * shape and row stride (both overwritten; y's contents are the beta term
+ * while timing).  It records for the current device the fastest kernel whose
+ * product agrees with the default's -- at beta = 0 and, when beta != 0, with
+ * the problem's beta from identical contents; fp32 output: every row and
+ * column within 1e-5 relative; fp16 output: every element within one fp16
+ * ulp and the whole within 1e-4 -- and writes its solution index to
+ * *solution_out (INT_MIN: the default) when that is not NULL.  The tuner
  * synchronises the stream and fails during stream capture; tune before
- * capturing.  Every candidate is deterministic (rocBLAS atomics disabled).
- * The first call on a device creates the device's rocBLAS handle, and
- * rocBLAS sizes its workspace on first use of a problem: run each problem
- * once outside capture.  Neither function has a counterpart in the reference.
+ * capturing.  Every candidate is deterministic (rocBLAS atomics disabled),
+ * but the choice is by timing, so two processes may keep different kernels
+ * (outputs differing in the last bits).  Each device's rocBLAS handle gets a
+ * fixed 32 MiB workspace, allocated on the first call on that device and
+ * never freed, so graphs never point at memory rocBLAS has freed; only
+ * rocBLAS's default kernel of an untuned problem may use it, and such calls
+ * on two streams of one device must not overlap.  Neither function has a
+ * counterpart in the reference.
  */
 int sidon_gemm_nt(const void* x, int ldx, const void* w, int ldw, void* y, int ldy, int M, int N, int K, int dtype,
                   float beta, sidon_stream_t stream);
 int sidon_gemm_nt_tune(const void* x, int ldx, const void* w, int ldw, void* y, void* y_check, int ldy, int M,
                        int N, int K, int dtype, float beta, sidon_stream_t stream, int* solution_out);
+/*
+ * Record rocBLAS solution `solution` (an index sidon_gemm_nt_tune returned
+ * in an earlier run; INT_MIN = rocBLAS's default) for the problem
+ * (M, N, K, ldx, ldw, ldy, dtype, beta != 0) on the current device, so runs
+ * are reproducible.  The first sidon_gemm_nt call of the problem fails with
+ * SIDON_E_SHAPE if rocBLAS has no such kernel for it or the kernel needs a
+ * workspace.  No counterpart in the reference.
+ */
+int sidon_gemm_nt_pin(int M, int N, int K, int ldx, int ldw, int ldy, int dtype, int beta_nonzero,
+                      int solution);
 /*
  * Causal depthwise conv + LayerNorm + SiLU over B items of T frames:
  *

@@ -46,6 +46,7 @@ SIGNATURES = {
     "sidon_gemm_nt_tune": (ctypes.c_int, [_VP, ctypes.c_int, _VP, ctypes.c_int, _VP, _VP, ctypes.c_int, ctypes.c_int,
                                           ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_float, _VP,
                                           ctypes.POINTER(ctypes.c_int)]),
+    "sidon_gemm_nt_pin": (ctypes.c_int, [ctypes.c_int] * 9),
     "sidon_causal_dw_norm": (ctypes.c_int, [_VP, ctypes.c_int, _VP, _VP, _VP, ctypes.c_float, _VP,
                                             ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _VP]),
     "sidon_fbank_frames": (ctypes.c_int, [_VP, _VP, ctypes.c_int, ctypes.c_int, _VP]),

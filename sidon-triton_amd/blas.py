@@ -19,13 +19,23 @@ made while the stream is not capturing, times rocBLAS's kernels for it on
 scratch tensors shaped like ``out`` and keeps the fastest one whose product
 agrees with rocBLAS's default (``sidon_gemm_nt_tune``; the scratch lives only
 for that call).  Later calls, and calls during capture, launch the kept
-kernel, or rocBLAS's default before a problem is tuned.  Every candidate is deterministic.  SIDON_GEMM_TUNE=0 in
-the environment keeps rocBLAS's default kernels.
+kernel, or rocBLAS's default before a problem is tuned.  Every candidate is
+deterministic and needs no workspace.  SIDON_GEMM_TUNE=0 in the environment
+keeps rocBLAS's default kernels.
+
+The choice is made by timing, so two processes (or boxes) may keep different
+kernels whose outputs differ in the last bits: results are not
+bit-reproducible across processes while tuning is on.  ``chosen_kernels()``
+returns the kernel kept per problem, and SIDON_GEMM_PIN=<file.json> (a map
+from ``problem_name(key)`` to a rocBLAS solution index, e.g. written from
+``chosen_kernels()`` of an earlier run) pins those problems to the given
+kernels instead of timing them.
 """
 
 from __future__ import annotations
 
 import ctypes
+import json
 import os
 
 import torch
@@ -40,6 +50,29 @@ _DTYPES = {
     (torch.float16, torch.float32): 2,
 }
 _tuned: set = set()
+_chosen: dict = {}      # problem key -> rocBLAS solution index (INT_MIN: rocBLAS's default)
+_pins = None            # SIDON_GEMM_PIN contents, read on first use
+
+
+def problem_name(key) -> str:
+    """'M,N,K,ldx,ldw,ldy,dtype,beta_nonzero' of a problem key (device omitted)."""
+    return ",".join(str(int(v)) for v in key[1:])
+
+
+def chosen_kernels() -> dict:
+    """{problem_name: solution index} of the problems tuned or pinned in this process."""
+    return {problem_name(k): v for k, v in _chosen.items()}
+
+
+def _pinned(key):
+    global _pins
+    if _pins is None:
+        path = os.environ.get("SIDON_GEMM_PIN")
+        _pins = {}
+        if path:
+            with open(path) as f:
+                _pins = {str(k): int(v) for k, v in json.load(f).items()}
+    return _pins.get(problem_name(key))
 
 
 def tuning_enabled() -> bool:
@@ -69,6 +102,12 @@ def gemm_nt(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor, beta: float = 0
     key = (device.index, m, n, k, x.stride(0), w.stride(0), out.stride(0), dtype, beta != 0.0)
     with torch.cuda.device(device):
         stream = _stream_handle(device)
+        pin = _pinned(key) if key not in _tuned else None
+        if pin is not None:
+            _lib.check("sidon_gemm_nt_pin", lib.sidon_gemm_nt_pin(m, n, k, x.stride(0), w.stride(0), out.stride(0),
+                                                                  dtype, int(beta != 0.0), pin))
+            _tuned.add(key)
+            _chosen[key] = pin
         if key not in _tuned and tuning_enabled() and not torch.cuda.is_current_stream_capturing():
             scratch = torch.zeros(2, m, out.stride(0), device=device, dtype=out.dtype)
             solution = ctypes.c_int(0)
@@ -76,6 +115,7 @@ def gemm_nt(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor, beta: float = 0
                                         dtype, float(beta), stream, ctypes.byref(solution))
             _lib.check("sidon_gemm_nt_tune", rc)
             _tuned.add(key)
+            _chosen[key] = solution.value
         rc = lib.sidon_gemm_nt(*head, out.data_ptr(), out.stride(0), m, n, k, dtype, float(beta), stream)
     _lib.check("sidon_gemm_nt", rc)
     return out

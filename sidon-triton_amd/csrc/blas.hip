@@ -15,6 +15,19 @@
 // with the default's; it synchronises the stream and must not run during
 // stream capture.  Handles are created with atomics
 // disallowed, so every candidate is deterministic (no split-K by atomics).
+//
+// Device memory.  Each device's handle gets a fixed workspace of
+// kWorkspaceBytes that this library allocates once and never frees, so
+// rocBLAS never reallocates (and frees) memory that a captured graph still
+// points to.  The tuner keeps only kernels that need no workspace at all
+// (rocBLAS's device-memory size query), so a tuned problem shares no memory
+// between streams; only rocBLAS's default kernel of an untuned problem may
+// use the workspace, and such calls on two streams of one device must not
+// overlap.
+//
+// The kept kernel is chosen by timing, so two processes may keep different
+// kernels whose outputs differ in the last bits; sidon_gemm_nt_pin records a
+// given kernel for a problem instead (reproducible runs).
 
 #define ROCBLAS_BETA_FEATURES_API  // rocblas_gemm_ex_get_solutions
 #include <hip/hip_runtime.h>
@@ -26,6 +39,7 @@
 #include <cstring>
 #include <map>
 #include <mutex>
+#include <set>
 #include <tuple>
 #include <vector>
 
@@ -40,6 +54,7 @@ using sidon::fail;
 
 constexpr int kMaxDevices = 64;
 constexpr int kDefault = INT_MIN;  // "rocBLAS's own choice" in the problem table
+constexpr size_t kWorkspaceBytes = size_t(32) << 20;
 
 struct Problem {
   const void* x;
@@ -61,7 +76,9 @@ Key key_of(int dev, const Problem& p) {
 
 std::mutex g_mu;  // guards the handles (one stream binding at a time) and the table
 rocblas_handle g_handle[kMaxDevices] = {};
+void* g_workspace[kMaxDevices] = {};  // held until the process ends
 std::map<Key, int> g_choice;
+std::set<Key> g_checked;  // problems whose recorded kernel needs no workspace
 
 rocblas_datatype in_type(int dtype) { return dtype == 0 ? rocblas_datatype_f32_r : rocblas_datatype_f16_r; }
 rocblas_datatype out_type(int dtype) { return dtype == 1 ? rocblas_datatype_f16_r : rocblas_datatype_f32_r; }
@@ -75,6 +92,15 @@ int handle_for(int dev, rocblas_handle* h) {
     if (rocblas_set_atomics_mode(nh, rocblas_atomics_not_allowed) != rocblas_status_success) {
       rocblas_destroy_handle(nh);
       return fail(SIDON_E_LAUNCH, "rocblas_set_atomics_mode failed on device %d", dev);
+    }
+    if (g_workspace[dev] == nullptr && hipMalloc(&g_workspace[dev], kWorkspaceBytes) != hipSuccess) {
+      g_workspace[dev] = nullptr;
+      rocblas_destroy_handle(nh);
+      return fail(SIDON_E_LAUNCH, "workspace allocation of %zu bytes failed on device %d", kWorkspaceBytes, dev);
+    }
+    if (rocblas_set_workspace(nh, g_workspace[dev], kWorkspaceBytes) != rocblas_status_success) {
+      rocblas_destroy_handle(nh);
+      return fail(SIDON_E_LAUNCH, "rocblas_set_workspace failed on device %d", dev);
     }
     g_handle[dev] = nh;
   }
@@ -90,6 +116,18 @@ rocblas_status run(rocblas_handle h, const Problem& p, int solution) {
                          p.ldy, p.y, out_type(p.dtype), p.ldy, rocblas_datatype_f32_r,
                          dflt ? rocblas_gemm_algo_standard : rocblas_gemm_algo_solution_index, dflt ? 0 : solution,
                          rocblas_gemm_flags_none);
+}
+
+// Device memory (bytes) kernel `solution` needs for p, from rocBLAS's size
+// query (the call is not executed); SIZE_MAX when the query fails.
+size_t workspace_need(rocblas_handle h, const Problem& p, int solution) {
+  size_t bytes = SIZE_MAX;
+  if (rocblas_start_device_memory_size_query(h) != rocblas_status_success) return SIZE_MAX;
+  const rocblas_status st = run(h, p, solution);
+  if (rocblas_stop_device_memory_size_query(h, &bytes) != rocblas_status_success ||
+      (st != rocblas_status_success && st != rocblas_status_size_unchanged && st != rocblas_status_size_increased))
+    return SIZE_MAX;
+  return bytes;
 }
 
 int validate(const Problem& p) {
@@ -165,16 +203,53 @@ bool read_rows(const Problem& p, hipStream_t s, std::vector<float>* out) {
   return true;
 }
 
-// ||a - b|| / ||b|| (0 when both are zero); non-finite values fail the gate.
-double rel_diff(const std::vector<float>& a, const std::vector<float>& b) {
-  double num = 0.0, den = 0.0;
-  for (size_t i = 0; i < a.size(); ++i) {
-    if (!std::isfinite(a[i]) || !std::isfinite(b[i])) return 1e30;
-    const double d = (double)a[i] - (double)b[i];
-    num += d * d;
-    den += (double)b[i] * b[i];
+// Agreement of a candidate's M x N product `got` with the default's `want`.
+// fp32 output: every row and every column within 1e-5 relative (per line,
+// so quiet lines -- the quiet frequency bins of the framing GEMM -- are held
+// to the bar as much as loud ones; a line whose reference energy is below
+// 1e-12 of the average is compared against that floor).  fp16 output: every
+// element within one fp16 ulp of the reference (fp32 sums in another order
+// move a value across a rounding boundary at most), and the whole product
+// within 1e-4 relative, which a kernel that rounds each product to fp16
+// (about 1.4e-4) does not meet.  Non-finite values fail.
+bool agrees(const std::vector<float>& got, const std::vector<float>& want, int M, int N, bool fp16_out) {
+  double tot = 0.0, num_all = 0.0;
+  for (size_t i = 0; i < want.size(); ++i) {
+    if (!std::isfinite(got[i]) || !std::isfinite(want[i])) return false;
+    tot += (double)want[i] * want[i];
+    const double d = (double)got[i] - (double)want[i];
+    num_all += d * d;
   }
-  return den > 0.0 ? std::sqrt(num / den) : (num > 0.0 ? 1e30 : 0.0);
+  if (fp16_out) {
+    for (size_t i = 0; i < want.size(); ++i) {
+      const float a = std::fabs(want[i]);
+      // spacing of fp16 values at |want| (2^-24 below the normal range)
+      const float ulp = a < 6.103515625e-05f ? 5.9604644775390625e-08f : std::ldexp(1.0f, std::ilogb(a) - 10);
+      if (std::fabs(got[i] - want[i]) > ulp) return false;
+    }
+    return tot > 0.0 ? std::sqrt(num_all / tot) <= 1e-4 : num_all == 0.0;
+  }
+  const double avg = tot / (double)want.size();
+  auto line_ok = [&](double num, double den, int count) {
+    const double floor = 1e-12 * avg * count;
+    return std::sqrt(num / std::max(den, floor > 0.0 ? floor : 1e-300)) <= 1e-5;
+  };
+  std::vector<double> cnum(N, 0.0), cden(N, 0.0);
+  for (int m = 0; m < M; ++m) {
+    double rnum = 0.0, rden = 0.0;
+    for (int n = 0; n < N; ++n) {
+      const size_t i = (size_t)m * N + n;
+      const double d = (double)got[i] - (double)want[i], r = (double)want[i] * want[i];
+      rnum += d * d;
+      rden += r;
+      cnum[n] += d * d;
+      cden[n] += r;
+    }
+    if (!line_ok(rnum, rden, N)) return false;
+  }
+  for (int n = 0; n < N; ++n)
+    if (!line_ok(cnum[n], cden[n], M)) return false;
+  return true;
 }
 
 }  // namespace
@@ -188,8 +263,15 @@ SIDON_API int sidon_gemm_nt(const void* x, int ldx, const void* w, int ldw, void
   std::lock_guard<std::mutex> lock(g_mu);
   rocblas_handle h;
   if ((rc = handle_for(dev, &h))) return rc;
-  const auto it = g_choice.find(key_of(dev, p));
+  const Key key = key_of(dev, p);
+  const auto it = g_choice.find(key);
   const int solution = it == g_choice.end() ? kDefault : it->second;
+  if (solution != kDefault && g_checked.count(key) == 0) {  // a pinned kernel, first call
+    const size_t need = workspace_need(h, p, solution);
+    if (need == SIZE_MAX) return fail(SIDON_E_SHAPE, "rocBLAS has no kernel %d for this problem", solution);
+    if (need != 0) return fail(SIDON_E_SHAPE, "kernel %d needs %zu bytes of workspace", solution, need);
+    g_checked.insert(key);
+  }
   if (rocblas_set_stream(h, reinterpret_cast<hipStream_t>(stream)) != rocblas_status_success)
     return fail(SIDON_E_LAUNCH, "rocblas_set_stream failed");
   const rocblas_status st = run(h, p, solution);
@@ -236,6 +318,16 @@ SIDON_API int sidon_gemm_nt_tune(const void* x, int ldx, const void* w, int ldw,
     }
   }
 
+  // Only kernels that need no device memory beyond their operands: a kernel
+  // that used the handle's workspace would share it between streams.
+  {
+    std::vector<int> kept;
+    for (const int c : cand)
+      if (workspace_need(h, p, c) == 0) kept.push_back(c);
+    cand.swap(kept);
+  }
+  if (cand.empty()) return fail(SIDON_E_LAUNCH, "every rocBLAS kernel for this problem needs a workspace");
+
   hipEvent_t e0 = nullptr, e1 = nullptr;
   if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) {
     if (e0) hipEventDestroy(e0);
@@ -260,26 +352,39 @@ SIDON_API int sidon_gemm_nt_tune(const void* x, int ldx, const void* w, int ldw,
   hipEventDestroy(e0);
   hipEventDestroy(e1);
   std::sort(timed.begin(), timed.end());
-  // Accuracy gate: the fastest candidate whose product (beta = 0) agrees with
-  // the default's to fp32-sum accuracy (fp16 rounding for an fp16 output).
-  // Some kernels for degenerate shapes (a single row) round the product to
-  // the operand type first; they are never chosen.
+  // Accuracy gate (agrees()): the fastest candidate whose product agrees with
+  // the default's at beta = 0 and, for a problem with beta != 0, also with
+  // the problem's beta from identical starting contents.  Some kernels for
+  // degenerate shapes (a single row) round the product to the operand type
+  // first; they are never chosen.
   Problem ref = p, trial = p;
   ref.y = y_check;
   ref.beta = trial.beta = 0.f;
+  const size_t esz = p.dtype == 1 ? 2 : 4;
+  // candidate c with the real beta vs the default with it, both starting
+  // from the contents y holds now (copied into y_check)
+  auto beta_ok = [&](int c) {
+    if (p.beta == 0.f || c == kDefault) return true;
+    std::vector<float> want_b, got_b;
+    Problem rb = p;
+    rb.y = y_check;
+    return hipMemcpy2DAsync(y_check, (size_t)p.ldy * esz, p.y, (size_t)p.ldy * esz, (size_t)p.N * esz,
+                            (size_t)p.M, hipMemcpyDeviceToDevice, s) == hipSuccess &&
+           run(h, rb, kDefault) == rocblas_status_success && read_rows(rb, s, &want_b) &&
+           run(h, p, c) == rocblas_status_success && read_rows(p, s, &got_b) &&
+           agrees(got_b, want_b, p.M, p.N, p.dtype == 1);
+  };
   int best = kDefault;
   bool found = false;
-  if (!timed.empty() && run(h, ref, kDefault) == rocblas_status_success) {
-    std::vector<float> want, got;
-    if (read_rows(ref, s, &want)) {
-      const double tol = p.dtype == 1 ? 2e-3 : 1e-5;
-      for (const auto& t : timed) {
-        if (t.second == kDefault || (run(h, trial, t.second) == rocblas_status_success && read_rows(trial, s, &got) &&
-                                     rel_diff(got, want) <= tol)) {
-          best = t.second;
-          found = true;
-          break;
-        }
+  std::vector<float> want, got;
+  if (!timed.empty() && run(h, ref, kDefault) == rocblas_status_success && read_rows(ref, s, &want)) {
+    for (const auto& t : timed) {
+      if (t.second == kDefault || (run(h, trial, t.second) == rocblas_status_success &&
+                                   read_rows(trial, s, &got) && agrees(got, want, p.M, p.N, p.dtype == 1) &&
+                                   beta_ok(t.second))) {
+        best = t.second;
+        found = true;
+        break;
       }
     }
   }
@@ -287,6 +392,28 @@ SIDON_API int sidon_gemm_nt_tune(const void* x, int ldx, const void* w, int ldw,
   if (!found || err != hipSuccess)
     return fail(SIDON_E_LAUNCH, "no rocBLAS kernel ran correctly for this problem (%s)", hipGetErrorString(err));
   g_choice[key_of(dev, p)] = best;
+  g_checked.insert(key_of(dev, p));
   if (solution_out) *solution_out = best;
+  return SIDON_OK;
+}
+
+SIDON_API int sidon_gemm_nt_pin(int M, int N, int K, int ldx, int ldw, int ldy, int dtype, int beta_nonzero,
+                                int solution) {
+  sidon::clear_error();
+  int rc, dev = 0;
+  if (M < 1 || N < 1 || K < 1 || dtype < 0 || dtype > 2)
+    return fail(SIDON_E_SHAPE, "M=%d, N=%d and K=%d must be >= 1 and dtype=%d in {0, 1, 2}", M, N, K, dtype);
+  if (ldx < K || ldw < K || ldy < N) return fail(SIDON_E_STRIDE, "row strides shorter than the rows");
+  if ((rc = sidon::check_device()) || (rc = current_device(&dev))) return rc;
+  std::lock_guard<std::mutex> lock(g_mu);
+  const Key key{dev, M, N, K, ldx, ldw, ldy, dtype, beta_nonzero != 0};
+  if (solution == kDefault) {
+    g_choice[key] = kDefault;
+    return SIDON_OK;
+  }
+  // Checked on the first call of the problem (sidon_gemm_nt): the kernel
+  // must exist for it and need no workspace.
+  g_checked.erase(key);
+  g_choice[key] = solution;
   return SIDON_OK;
 }

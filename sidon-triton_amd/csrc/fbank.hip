@@ -1,6 +1,7 @@
 // fbank.hip -- the encoder's fbank front end around its framing GEMM
 // (MI355X / gfx950).  The framing GEMM (frames [R, 400] x the [400, 514]
-// DC-removal / pre-emphasis / window / rDFT matrix, fp32) runs in hipBLASLt;
+// DC-removal / pre-emphasis / window / rDFT matrix, fp32) runs on rocBLAS
+// (sidon_gemm_nt, the kernel chosen by timing);
 // these kernels do the rest of src/sidon_triton/frontend.py:218-240:
 //
 //   logmel     spec [R, 514] (re 257 | im 257) -> log(max(power . mel, 1.19e-7)) [R, 80]

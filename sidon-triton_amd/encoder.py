@@ -16,7 +16,9 @@ Mirrors src/sidon_triton/triton_encoder.py:
     ``load_encoder`` also reads the reference's own ``encoder_triton.pt``
     (with ``torch.load(weights_only=True)``).
 
-Per layer the work is: res_norm (HIP), hipBLASLt GEMMs through torch, the
+Per layer the work is: res_norm (HIP), hipBLASLt GEMMs through torch (QKV,
+the residual projections), the pointwise conv's first GEMM on rocBLAS with
+the kernel chosen by timing (``blas.gemm_nt``), the
 feed-forward input projections with bias and SiLU (one HIP GEMM kernel where
 its tiles fill the chip, else hipBLASLt followed by the in-place HIP SiLU),
 the relative_key attention (HIP), and the conv module's GLU + causal

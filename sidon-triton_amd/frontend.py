@@ -8,7 +8,8 @@ to a bucket of S samples (S a multiple of 320) with their true lengths:
      with hop 160 -> [B, S / 160, 400];
   2. framing GEMM with the constant [400, 514] matrix of ``frame_transform``
      (DC removal, pre-emphasis 0.97, Povey window, 512-point rDFT, x 2^15),
-     fp32 in hipBLASLt (gfx950 has no reduced-precision fp32 GEMM path, so
+     fp32 on rocBLAS with the kernel chosen by timing (``blas.gemm_nt``;
+     gfx950 has no reduced-precision fp32 GEMM path, so
      the quiet bins keep full fp32, as frontend.py:178-180 requires);
   3. ``sidon_fbank_logmel`` (HIP): power, 80 Kaldi mel bins (sparse
      triangles), log(max(., 1.19e-7));
@@ -123,8 +124,9 @@ class Fbank:
         if device.type == "cuda" and device.index is None:
             device = torch.device("cuda", torch.cuda.current_device())
         self.device = device
-        # Kept as [514, 400] and used transposed: hipBLASLt picks a faster kernel
-        # for this operand order (57.5 against 59.6 us at a 96 s chunk).
+        # Kept as [514, 400] (rows K-contiguous), the w operand of
+        # blas.gemm_nt (y = x . w^T); this order was also the faster one when
+        # the GEMM ran on hipBLASLt (57.5 against 59.6 us at a 96 s chunk).
         self.weight_t = frame_transform().float().t().contiguous().to(device)
         lo, length, weights = sparse_mel(mel_banks())
         self.mel_lo = torch.from_numpy(lo).to(device)

@@ -272,6 +272,18 @@ def test_gemm_nt_rejects_bad_arguments_before_launch(sidon, over, code):
     assert _call(lib, "sidon_gemm_nt_tune", tune_base, over) == code
 
 
+@pytest.mark.parametrize("over,code", [
+    (dict(M=0), -2),
+    (dict(K=-1), -2),
+    (dict(dtype=3), -2),
+    (dict(ldx=100), -3),
+    (dict(ldy=100), -3),
+])
+def test_gemm_nt_pin_rejects_bad_arguments(sidon, over, code):
+    base = dict(M=4800, N=1024, K=4096, ldx=4096, ldw=4096, ldy=1024, dtype=2, beta_nonzero=1, solution=7)
+    assert _call(sidon._lib.load(), "sidon_gemm_nt_pin", base, over) == code
+
+
 def test_gemm_nt_wrapper_rejects_bad_tensors(sidon):
     """blas.gemm_nt checks devices, types and shapes in Python, before any
     library call (host tensors never reach the C ABI)."""

@@ -127,3 +127,34 @@ def test_tuner_refuses_to_run_during_capture(sidon):
     assert rc == -5 and "capture" in msg, (rc, msg)
     graph.replay()
     torch.cuda.synchronize()
+
+
+def test_pinned_kernel_reproduces_the_tuned_one(sidon, monkeypatch, tmp_path):
+    """SIDON_GEMM_PIN pins a problem to a given rocBLAS kernel: pinning the
+    kernel the tuner kept for one problem onto the same product with another
+    output row stride (a different problem key) gives bit-identical values,
+    and chosen_kernels() reports both.  A kernel index rocBLAS does not have
+    is refused on the first call."""
+    import json
+
+    x, w, y0 = _problem(1500, 1024, 1024, torch.float16, torch.float32, seed=21)
+    out = y0.clone()
+    sidon.blas.gemm_nt(x, w, out, beta=1.0)
+    key = (DEV.index, 1500, 1024, 1024, x.stride(0), w.stride(0), out.stride(0), 2, True)
+    tuned = sidon.blas.chosen_kernels()[sidon.blas.problem_name(key)]
+    wide = torch.empty(1500, 1040, device=DEV)[:, :1024]
+    wide.copy_(y0)
+    key2 = key[:6] + (wide.stride(0),) + key[7:]
+    bad = torch.empty(1500, 1056, device=DEV)[:, :1024]
+    key3 = key[:6] + (bad.stride(0),) + key[7:]
+    pins = tmp_path / "pins.json"
+    pins.write_text(json.dumps({sidon.blas.problem_name(key2): tuned, sidon.blas.problem_name(key3): 10 ** 9}))
+    monkeypatch.setenv("SIDON_GEMM_PIN", str(pins))
+    monkeypatch.setattr(sidon.blas, "_pins", None)
+    sidon.blas.gemm_nt(x, w, wide, beta=1.0)
+    torch.cuda.synchronize()
+    assert torch.equal(wide, out)
+    assert sidon.blas.chosen_kernels()[sidon.blas.problem_name(key2)] == tuned
+    with pytest.raises(sidon._lib.SidonError) as exc:
+        sidon.blas.gemm_nt(x, w, bad, beta=1.0)
+    assert exc.value.code == -2
