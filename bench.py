@@ -66,6 +66,37 @@ def qkv_of(torch, h, proj, out=None):
     return torch.matmul(x.half(), proj.t(), out=out)
 
 
+def c3_workload(torch, sidon, dev):
+    """The c3 chunk as benched: per layer l, q/k/v = qkv_of(h_l) with h_0 the
+    seeded stream and h_{l+1} = h_l + ctx_l (computed once, untimed, so every
+    layer's inputs are resident before timing), and one captured graph of
+    the 8 attention calls on those inputs.  Parity of this chain and graph:
+    tests/test_workloads_gpu.py."""
+    h0, rels, projs = build_inputs(torch)
+    rels_d = [r.to(dev) for r in rels]
+    projs_d = [p.to(dev) for p in projs]
+    outs = [torch.empty(B * L, H * D, dtype=torch.float16, device=dev) for _ in range(LAYERS)]
+    lens = torch.full((B,), L, dtype=torch.int32, device=dev)
+    attn = sidon.encoder_attention.flexrel_attention
+    with torch.no_grad():
+        h = h0.to(dev)
+        qkv = []
+        for i in range(LAYERS):
+            qkv.append(qkv_of(torch, h, projs_d[i]))
+            attn(qkv[i], B, H, rels_d[i], lens, out=outs[i])
+            h = h + outs[i].float()
+    torch.cuda.synchronize()
+
+    def enqueue_attention():
+        for i in range(LAYERS):
+            attn(qkv[i], B, H, rels_d[i], lens, out=outs[i])
+
+    graphs = sidon.graphs.BucketGraphs()
+    graph = graphs.capture(("attn", L), enqueue_attention)
+    return {"h0": h0, "rels": rels, "rels_d": rels_d, "projs_d": projs_d, "qkv": qkv, "outs": outs,
+            "lens": lens, "attn": attn, "graphs": graphs, "graph": graph}
+
+
 def cpu_baseline(torch, qkv0, rel0, heads):
     """Time the fp32 torch restatement on `heads` heads of layer 0; scale to a chunk."""
     from oracle.flexrel_oracle import torch_core_chunked
@@ -109,12 +140,15 @@ def c4_clips(count=128, rate=16000, source_seconds=64.0):
     return clips
 
 
-def run_c4(torch, sidon, args) -> dict:
-    """128 clips, batch 1 each, 8 layers of attention per clip; one graph per
-    bucket (L) that reads the clip's LK from a device buffer set before each
-    replay.  Inputs per bucket: seeded fp16 q/k/v ~N(0,1) per layer and the
-    per-layer tables of c3."""
-    dev = torch.device("cuda:0")
+def c4_workload(torch, sidon, dev):
+    """The c4 clips and, per bucket L, the state its captured graph runs on:
+    seeded fp16 q/k/v ~N(0,1) per layer ([L, 3*16*64], fused layout), the
+    per-layer tables of c3, outputs [L, 1024] and a device length vector
+    that the caller sets to the clip's LK before each replay.
+    Returns (clips, {L: (qkv, outs, lens, graph)}, keep) with keep =
+    {"rels": host tables, "rels_d": device tables, "graphs": BucketGraphs}:
+    the graphs read rels_d, so the caller holds ``keep`` as long as it
+    replays them."""
     clips = c4_clips()
     buckets = sorted({L for L, _ in clips})
     _, rels, _ = build_inputs(torch)
@@ -132,6 +166,18 @@ def run_c4(torch, sidon, args) -> dict:
             for i in range(LAYERS):
                 attn(qkv[i], 1, H, rels_d[i], lens, out=outs[i])
         state[L] = (qkv, outs, lens, graphs.capture(("c4", L), enqueue))
+    return clips, state, {"rels": rels, "rels_d": rels_d, "graphs": graphs}
+
+
+def run_c4(torch, sidon, args) -> dict:
+    """128 clips, batch 1 each, 8 layers of attention per clip; one graph per
+    bucket (L) that reads the clip's LK from a device buffer set before each
+    replay.  Inputs per bucket: seeded fp16 q/k/v ~N(0,1) per layer and the
+    per-layer tables of c3 (c4_workload).  Parity of these graphs:
+    tests/test_workloads_gpu.py."""
+    dev = torch.device("cuda:0")
+    clips, state, keep = c4_workload(torch, sidon, dev)  # noqa: F841 (keep: the graphs read it)
+    buckets = sorted(state)
     lens_all = torch.tensor([lk for _, lk in clips], dtype=torch.int32, device=dev)
     stream = torch.cuda.current_stream()
 
@@ -444,28 +490,9 @@ def main() -> int:
     shape = sidon._lib.launch_shape(B, H, L)
     log(f"launch shape at L={L}: {shape}; {sidon._lib.version()}")
 
-    h0, rels, projs = build_inputs(torch)
-    rels_d = [r.to(dev) for r in rels]
-    projs_d = [p.to(dev) for p in projs]
-    outs = [torch.empty(B * L, H * D, dtype=torch.float16, device=dev) for _ in range(LAYERS)]
-    lens = torch.full((B,), L, dtype=torch.int32, device=dev)
-    attn = sidon.encoder_attention.flexrel_attention
-    # Untimed: every layer's q/k/v, resident in HBM before timing starts.
-    with torch.no_grad():
-        h = h0.to(dev)
-        qkv = []
-        for i in range(LAYERS):
-            qkv.append(qkv_of(torch, h, projs_d[i]))
-            attn(qkv[i], B, H, rels_d[i], lens, out=outs[i])
-            h = h + outs[i].float()
-    torch.cuda.synchronize()
-
-    def enqueue_attention():
-        for i in range(LAYERS):
-            attn(qkv[i], B, H, rels_d[i], lens, out=outs[i])
-
-    graphs = sidon.graphs.BucketGraphs()
-    graph = graphs.capture(("attn", L), enqueue_attention)
+    w = c3_workload(torch, sidon, dev)
+    h0, rels, projs_d, qkv, outs, lens = w["h0"], w["rels"], w["projs_d"], w["qkv"], w["outs"], w["lens"]
+    rels_d, attn, graphs, graph = w["rels_d"], w["attn"], w["graphs"], w["graph"]
     stream = torch.cuda.current_stream()
     for _ in range(args.warmup):
         graph.replay()

@@ -10,6 +10,12 @@ LRU of 128.
 The attention entry points are capture-safe: they launch on the current
 stream, allocate nothing inside the library and never read device data on the
 host, so a whole sequence of layers is one graph per bucket.
+
+A graph holds raw device addresses of every tensor its work touched.  Each
+graph is therefore kept together with the ``enqueue`` callable it was
+captured from: whatever that callable references (its tensors, directly or
+through a closure) stays alive exactly as long as the graph, and is never
+freed and reused under a later replay.
 """
 
 from __future__ import annotations
@@ -30,10 +36,10 @@ class BucketGraphs:
         return len(self._graphs)
 
     def capture(self, key: Hashable, enqueue: Callable[[], None]) -> torch.cuda.CUDAGraph:
-        graph = self._graphs.get(key)
-        if graph is not None:
+        entry = self._graphs.get(key)
+        if entry is not None:
             self._graphs.move_to_end(key)
-            return graph
+            return entry[0]
         current = torch.cuda.current_stream()
         side = torch.cuda.Stream()
         side.wait_stream(current)
@@ -46,7 +52,7 @@ class BucketGraphs:
             self._pool = torch.cuda.graph_pool_handle()
         with torch.cuda.graph(graph, pool=self._pool):
             enqueue()
-        self._graphs[key] = graph
+        self._graphs[key] = (graph, enqueue)
         while len(self._graphs) > self.max_graphs:
             self._graphs.popitem(last=False)
         return graph
