@@ -185,6 +185,21 @@ size_t sidon_fbank_workspace_bytes(int B, int F);
 int sidon_fbank_normalize(const float* logmel, const int* valid, float* workspace, size_t workspace_bytes,
                           float* feats, int B, int F, sidon_stream_t stream);
 
+/*
+ * sidon_fbank_normalize without a workspace argument: the same kernels and
+ * results (bit for bit), with the statistics held in a static device array
+ * of the library (1.9 MiB per device, kept until the process ends) instead
+ * of caller memory.  No counterpart in the reference: it is for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops).  It allocates nothing and calls no allocating routine.  B <= 32
+ * items (any F); larger B returns SIDON_E_SHAPE.  Every call on one device
+ * shares that device's array, so calls that overlap on one GPU (two streams,
+ * two threads) race; every word a call reads is written earlier in the same
+ * call, so consecutive calls need no clearing.
+ */
+int sidon_fbank_normalize_noalloc(const float* logmel, const int* valid, float* feats, int B, int F,
+                                  sidon_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -53,6 +53,7 @@ SIGNATURES = {
     "sidon_fbank_logmel": (ctypes.c_int, [_VP, _VP, _VP, _VP, ctypes.c_int, _VP, ctypes.c_int, _VP]),
     "sidon_fbank_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int, ctypes.c_int]),
     "sidon_fbank_normalize": (ctypes.c_int, [_VP, _VP, _VP, ctypes.c_size_t, _VP, ctypes.c_int, ctypes.c_int, _VP]),
+    "sidon_fbank_normalize_noalloc": (ctypes.c_int, [_VP, _VP, _VP, ctypes.c_int, ctypes.c_int, _VP]),
     "sidon_last_error": (ctypes.c_char_p, []),
     "sidon_version": (ctypes.c_char_p, []),
 }

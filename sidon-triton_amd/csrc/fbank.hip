@@ -22,6 +22,8 @@
 
 #include <stdint.h>
 
+#include <mutex>
+
 #include "sidon_encoder.h"
 #include "sidon_host.h"
 
@@ -304,6 +306,41 @@ __global__ void __launch_bounds__(kLanes * kMel) apply_kernel(const float* __res
 
 int tiles_for(int F) { return F / 128 < 1 ? 1 : (F / 128 > kMaxTiles ? kMaxTiles : F / 128); }
 
+// Scratch of sidon_fbank_normalize_noalloc: the normalize workspace of up
+// to kScratchItems items of any length (tiles_for() caps the tiles at
+// kMaxTiles), 1.9 MiB in all, one copy per device for the life of the
+// process.  Every word a call reads was written earlier in the same call, so
+// nothing needs clearing between calls.
+constexpr int kScratchItems = 32;
+constexpr size_t kScratchFloats = (size_t)kScratchItems * (kMaxTiles * kMel * 3 + kMel * 2);
+static __device__ __align__(256) float scratch[kScratchFloats];
+
+// Device address of `scratch` per device, taken once per device with that
+// device current (host code must never pass the symbol itself to a kernel).
+constexpr int kMaxDevices = 64;
+std::once_flag g_scratch_once[kMaxDevices];
+float* g_scratch[kMaxDevices] = {};
+hipError_t g_scratch_err[kMaxDevices] = {};
+
+int normalize_launch(const float* logmel, const int* valid, float* workspace, float* feats, int B, int F,
+                     hipStream_t s) {
+  using sidon::fail;
+  const int G = tiles_for(F);
+  hipLaunchKernelGGL(stats_kernel, dim3(G, B), dim3(kLanes * kMel), 0, s, logmel, valid, workspace, F, G);
+  hipError_t err = hipGetLastError();
+  if (err == hipSuccess) {
+    hipLaunchKernelGGL(merge_kernel, dim3(kMel / kMergeBins, B), dim3(kMergeThreads), 0, s, valid, workspace, F, G, B);
+    err = hipGetLastError();
+  }
+  if (err == hipSuccess) {
+    hipLaunchKernelGGL(apply_kernel, dim3((F + kApplyFrames - 1) / kApplyFrames, B), dim3(kLanes * kMel), 0, s,
+                       logmel, valid, workspace, feats, F, G, B);
+    err = hipGetLastError();
+  }
+  if (err != hipSuccess) return fail(SIDON_E_LAUNCH, "fbank normalize launch failed: %s", hipGetErrorString(err));
+  return SIDON_OK;
+}
+
 }  // namespace
 
 SIDON_API int sidon_fbank_logmel(const float* spec, const float* mel_w, const int* mel_lo, const int* mel_len,
@@ -363,19 +400,31 @@ SIDON_API int sidon_fbank_normalize(const float* logmel, const int* valid, float
   if (logmel == feats) return fail(SIDON_E_SHAPE, "feats must not alias logmel");
   int rc;
   if ((rc = sidon::check_device())) return rc;
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const int G = tiles_for(F);
-  hipLaunchKernelGGL(stats_kernel, dim3(G, B), dim3(kLanes * kMel), 0, s, logmel, valid, workspace, F, G);
-  hipError_t err = hipGetLastError();
-  if (err == hipSuccess) {
-    hipLaunchKernelGGL(merge_kernel, dim3(kMel / kMergeBins, B), dim3(kMergeThreads), 0, s, valid, workspace, F, G, B);
-    err = hipGetLastError();
-  }
-  if (err == hipSuccess) {
-    hipLaunchKernelGGL(apply_kernel, dim3((F + kApplyFrames - 1) / kApplyFrames, B), dim3(kLanes * kMel), 0, s,
-                       logmel, valid, workspace, feats, F, G, B);
-    err = hipGetLastError();
-  }
-  if (err != hipSuccess) return fail(SIDON_E_LAUNCH, "fbank normalize launch failed: %s", hipGetErrorString(err));
-  return SIDON_OK;
+  return normalize_launch(logmel, valid, workspace, feats, B, F, reinterpret_cast<hipStream_t>(stream));
+}
+
+SIDON_API int sidon_fbank_normalize_noalloc(const float* logmel, const int* valid, float* feats, int B, int F,
+                                            sidon_stream_t stream) {
+  using sidon::fail;
+  sidon::clear_error();
+  if (!logmel || !valid || !feats) return fail(SIDON_E_NULL, "every pointer must be non-NULL");
+  if (B < 1 || F < 2 || (F & 1) != 0) return fail(SIDON_E_SHAPE, "B=%d must be >= 1 and F=%d even and >= 2", B, F);
+  if (B > kScratchItems || sidon_fbank_workspace_bytes(B, F) > sizeof(scratch))
+    return fail(SIDON_E_SHAPE, "B=%d items exceed the %d the static scratch holds (use sidon_fbank_normalize)", B,
+                kScratchItems);
+  if (logmel == feats) return fail(SIDON_E_SHAPE, "feats must not alias logmel");
+  int rc;
+  if ((rc = sidon::check_device())) return rc;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(SIDON_E_DEVICE, "no usable HIP device");
+  std::call_once(g_scratch_once[dev], [dev]() {
+    void* ptr = nullptr;
+    g_scratch_err[dev] = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    g_scratch[dev] = g_scratch_err[dev] == hipSuccess ? static_cast<float*>(ptr) : nullptr;
+  });
+  if (g_scratch[dev] == nullptr)
+    return fail(SIDON_E_DEVICE, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                hipGetErrorString(g_scratch_err[dev]));
+  return normalize_launch(logmel, valid, g_scratch[dev], feats, B, F, reinterpret_cast<hipStream_t>(stream));
 }
