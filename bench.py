@@ -97,30 +97,116 @@ def c3_workload(torch, sidon, dev):
             "lens": lens, "attn": attn, "graphs": graphs, "graph": graph}
 
 
-def cpu_baseline(torch, qkv0, rel0, heads):
-    """Time the fp32 torch restatement on `heads` heads of layer 0; scale to a chunk."""
+def host_cpu() -> dict:
+    """This host's CPU: model and sockets from lscpu, os.cpu_count() and the
+    cores this process may run on (its affinity set)."""
+    import subprocess
+
+    info = {"cpu_count": os.cpu_count(), "affinity": len(os.sched_getaffinity(0)), "model": None,
+            "sockets": None, "cores_per_socket": None, "threads_per_core": None}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+    except (OSError, subprocess.SubprocessError):
+        return info
+    keys = {"Model name": "model", "Socket(s)": "sockets", "Core(s) per socket": "cores_per_socket",
+            "Thread(s) per core": "threads_per_core"}
+    for line in out.splitlines():
+        name, _, val = line.partition(":")
+        if name.strip() in keys and info[keys[name.strip()]] is None:
+            val = val.strip()
+            info[keys[name.strip()]] = int(val) if val.isdigit() else val
+    return info
+
+
+def _median_s(fn, runs, warmup=1):
+    for _ in range(warmup):
+        fn()
+    samples = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        samples.append(time.perf_counter() - t0)
+    return statistics.median(samples)
+
+
+def cpu_baseline(torch, qkv_host, rels) -> dict:
+    """The reference's CPU fp32 path (oracle.torch_core_chunked, the fp32
+    torch restatement of flexrel_triton.py:297-328, 512-row chunks) timed on
+    this host with one thread per core of the affinity set:
+      * c3: the whole chunk -- 8 layers x 16 heads at L=4800 on the benched
+        layers' own q/k/v (fp16 upcast), median of 3 after a one-layer
+        warm-up;
+      * c1: one call at L=750 on fp32 q/k/v ~N(0,1)/8, median of 5;
+      * c2: one call at L=1500 with 1463 valid keys (fp16 inputs upcast),
+        median of 3.
+    """
     from oracle.flexrel_oracle import torch_core_chunked
 
-    hid = H * D
-    view = qkv0.view(B, L, 3, H, D)
-    q, k, v = (view[:, :, i, :heads].permute(0, 2, 1, 3).float().contiguous() for i in range(3))
-    rel = rel0.float()
-    torch_core_chunked(q, k, v, rel)  # warm-up
-    samples = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        torch_core_chunked(q, k, v, rel)
-        samples.append(time.perf_counter() - t0)
-    per_head_layer_ms = statistics.median(samples) * 1e3 / heads
+    host = host_cpu()
+    threads = host["affinity"]
+    torch.set_num_threads(threads)
+    layers = []
+    for qkv, rel in zip(qkv_host, rels):
+        view = qkv.view(B, L, 3, H, D)
+        q, k, v = (view[:, :, i].permute(0, 2, 1, 3).float().contiguous() for i in range(3))
+        layers.append((q, k, v, rel.float()))
+
+    def chunk():
+        for q, k, v, rel in layers:
+            torch_core_chunked(q, k, v, rel)
+    torch_core_chunked(*layers[0])  # warm-up: one layer
+    c3_s = _median_s(chunk, 3, warmup=0)
+
+    gen = torch.Generator().manual_seed(101)
+    c1 = [torch.randn(1, H, 750, D, generator=gen) / 8 for _ in range(3)]
+    rel1 = torch.randn(73, D, generator=gen) * 0.02
+    c1_s = _median_s(lambda: torch_core_chunked(*c1, rel1), 5)
+    gen = torch.Generator().manual_seed(102)
+    c2 = [torch.randn(1, H, 1500, D, generator=gen).half().float() for _ in range(3)]
+    rel2 = (torch.randn(73, D, generator=gen) * 0.02).half().float()
+    c2_s = _median_s(lambda: torch_core_chunked(*c2, rel2, [1463]), 3)
     return {
-        "value": per_head_layer_ms * H * LAYERS,
+        "value": c3_s * 1e3,
         "unit": "ms per 96 s chunk",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": (f"layer 0, {heads} of {H} heads, L=4800, fp32 torch (oracle.torch_core_chunked, "
-                   f"512-row chunks); median of 3 after 1 warm-up = {statistics.median(samples):.3f} s; "
-                   f"scaled x{H * LAYERS // heads} to 8 layers x 16 heads"),
+        "sample": (f"the whole c3 chunk: 8 layers x 16 heads at L=4800 on the benched q/k/v, fp32 torch "
+                   f"(oracle.torch_core_chunked, 512-row chunks), median of 3 after a one-layer warm-up; "
+                   f"torch.set_num_threads({threads}) = this process's affinity set"),
+        "c1_ms_per_call": c1_s * 1e3,
+        "c2_ms_per_call": c2_s * 1e3,
+        "host": host,
     }
+
+
+def gpu_per_call(torch, sidon, dev) -> dict:
+    """Single attention calls at c1 (L=750, q/k/v ~N(0,1)/8 cast to fp16)
+    and c2 (L=1500, 1463 valid keys), each timed with events on its stream:
+    5 warm-up calls, then the median of 30 (engines.py:26-44)."""
+    attn = sidon.encoder_attention.flexrel_attention
+    res = {}
+    for name, length, valid, scale, seed in (("c1", 750, 750, 0.125, 101), ("c2", 1500, 1463, 1.0, 102)):
+        gen = torch.Generator().manual_seed(seed)
+        qkv = (torch.randn(length, 3 * H * D, generator=gen) * scale).half().to(dev)
+        rel = (torch.randn(73, D, generator=gen) * 0.02).half().to(dev)
+        lens = torch.full((1,), valid, dtype=torch.int32, device=dev)
+        out = torch.empty(length, H * D, dtype=torch.float16, device=dev)
+        stream = torch.cuda.current_stream()
+        for _ in range(5):
+            attn(qkv, 1, H, rel, lens, out=out)
+        torch.cuda.synchronize()
+        samples = []
+        for _ in range(30):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            attn(qkv, 1, H, rel, lens, out=out)
+            e1.record(stream)
+            e1.synchronize()
+            samples.append(e0.elapsed_time(e1) * 1e3)
+        us = statistics.median(samples)
+        res[name] = {"L": length, "valid": valid, "us": us,
+                     "tflops": attention_flops(H, valid, valid) / (us * 1e-6) / 1e12}
+    return res
 
 
 def c4_clips(count=128, rate=16000, source_seconds=64.0):
@@ -444,7 +530,6 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-heads", type=int, default=4)
     ap.add_argument("--no-check", action="store_true",
                     help="accepted for compatibility; parity is checked by tests/ (the oracle is used here only "
                          "for the CPU baseline)")
@@ -551,6 +636,8 @@ def main() -> int:
         c1.synchronize()
         extra["with_projections_ms"] = c0.elapsed_time(c1) / 10
 
+    extra["gpu_per_call_us"] = gpu_per_call(torch, sidon, dev)
+
     traffic = None
     if TRAFFIC_FILE.exists():
         import re
@@ -579,7 +666,7 @@ def main() -> int:
     result.update(extra)
     if not args.no_cpu_baseline:
         log("timing the CPU baseline ...")
-        result["cpu_baseline"] = cpu_baseline(torch, qkv[0].cpu(), rels[0], args.cpu_heads)
+        result["cpu_baseline"] = cpu_baseline(torch, [t.cpu() for t in qkv], rels)
     print(json.dumps(result), flush=True)
     return 0
 

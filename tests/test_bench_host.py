@@ -46,3 +46,12 @@ def test_encoder_model_weights_shapes():
     assert w["heads"] == 16 and w["fp_w"].shape == (1024, 160)
     assert p["ffn1_w1"].shape == (4096, 1024) and p["ffn2_w2"].shape == (1024, 4096)
     assert p["pw1_w"].shape == (2048, 1024) and p["dw_w"].shape == (1024, 31) and p["rel"].shape == (73, 64)
+
+
+def test_host_cpu_reports_this_host():
+    import os
+
+    info = bench.host_cpu()
+    assert info["cpu_count"] == os.cpu_count()
+    assert 1 <= info["affinity"] <= os.cpu_count()
+    assert info["model"] is None or isinstance(info["model"], str)
