@@ -1,0 +1,143 @@
+// flexrel_device.h -- device helpers and launch parameters shared by the
+// relative_key attention kernels (flexrel_fwd.hip: 64 query rows per
+// workgroup, 8 key splits; flexrel_wide.hip: 128 query rows per wavefront,
+// 4 key splits).  Internal to the library.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <stdint.h>
+
+namespace sidon_flexrel {
+
+constexpr int kD = 64;          // head dim
+constexpr int kLeft = 64;       // clamp window: j - i in [-64, 8]
+constexpr int kRight = 8;
+constexpr int kNumPos = 73;     // rows of the relative table
+constexpr int kStep = 32;       // keys per pipeline step
+constexpr int kTile = kStep * kD * 2;  // bytes of one K or V step tile (4 KB)
+constexpr int kQrStride = 76;   // fp32 per row of the q.rel table
+// A query's 32 probabilities of one step summing below 2^15 are each below
+// the fp16 maximum, so their fp16 rounding is finite; a larger (or
+// non-finite) sum sends the query through the exact max update.
+constexpr float kSumLimit = 32768.f;
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef short s4 __attribute__((ext_vector_type(4)));
+typedef float f2 __attribute__((ext_vector_type(2)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+#define SIDON_LDS_PTR(T, p) ((__attribute__((address_space(3))) T*)(p))
+
+struct Params {
+  const _Float16* q;
+  const _Float16* k;
+  const _Float16* v;
+  const _Float16* rel;
+  const int32_t* lens;
+  _Float16* out;
+  int64_t qsb, qsh;  // batch / head strides (elements)
+  int64_t ksb, ksh;
+  int64_t vsb, vsh;
+  int64_t osb, osh;
+  int qsl, ksl, vsl, osl;  // row strides (elements, < 2^25)
+  int B, H, L;
+  int nqb;                 // query blocks per (b, h) in this launch
+  int row0;                // first query row of block 0 (a launch may cover rows [row0, L))
+  float scale;             // log2(e) / sqrt(64)
+};
+
+// 16-byte chunk c of tile row r is stored at chunk position c ^ tile_swz(r)
+// (LDS: 64 banks of 4 bytes).  The map is a bijection of row bits 1..3, which
+// keeps the 16 rows of every 16-lane ds_read_b128 group on distinct banks.
+// It puts row bit 1 on chunk bit 2: a 32-lane half of a ds_read_b64_tr_b16
+// reads rows with bits 0-1 varying and chunk bits 0-1 varying (lane bits 1
+// and 4), so row bit 1 must land on the one chunk bit that does not vary.
+__device__ __forceinline__ int tile_swz(int row) {
+  return ((row >> 2) & 1) | ((row >> 2) & 2) | ((row << 1) & 4);
+}
+
+// Key row fed to A-operand lane m of S^T = K.Q^T: bits 2 and 3 of m swapped.
+// With the 32x32 accumulator layout (lane half g holds rows 8*(i/4) + 4g +
+// i%4) element i of lane half g is then key 16*(i >> 3) + 8g + (i & 7).
+__device__ __forceinline__ int mfma_row_perm(int m) {
+  return (m & 0x13) | ((m >> 1) & 4) | ((m << 1) & 8);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// x of lane l and of lane l ^ 32 (the other half of the wavefront) combined
+// with max.  v_permlane32_swap applied to (x, x) leaves one half's
+// value in each result register, so any symmetric combination of the two is
+// the combination over the lane pair.
+__device__ __forceinline__ float pair_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+// Asynchronous copy global -> LDS of one 4 KB tile: four instructions of
+// 64 lanes x 16 bytes.  Instruction i adds 1024 i to both addresses: lane l's
+// bytes gbase[voff_i,l + 1024 i .. +16) land at LDS byte address
+// lds_addr + 1024 i + 16 l.  Issued as inline assembly so that the compiler
+// does not wait for the copy before unrelated LDS reads; completion is
+// awaited with wait_vmcnt below.  M0 is written here; nothing else in the
+// library's kernels uses M0 (the clobber documents it -- the compiler treats
+// M0 as reserved).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma_tile(uint32_t lds_addr, const char* gbase, uint32_t v0, uint32_t v1,
+                                         uint32_t v2, uint32_t v3) {
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, %5\n\t"
+      "global_load_lds_dwordx4 %2, %5 offset:1024\n\t"
+      "global_load_lds_dwordx4 %3, %5 offset:2048\n\t"
+      "global_load_lds_dwordx4 %4, %5 offset:3072"
+      :: "s"(lds_addr), "v"(v0), "v"(v1), "v"(v2), "v"(v3), "s"(gbase) : "memory", "m0");
+}
+__device__ __forceinline__ void dma_1k(uint32_t lds_addr, const char* gbase, uint32_t v0) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+               :: "s"(lds_addr), "v"(v0), "s"(gbase) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory");
+}
+
+__device__ __forceinline__ void wait_lgkm0() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+}
+
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+__device__ __forceinline__ h8 cat(h4 a, h4 b) {
+  return h8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+
+// Workgroups are dispatched round-robin over the 8 XCDs; linear work index
+// of workgroup `bid` such that each XCD gets a contiguous range (one head's
+// K/V then stays in one XCD's L2).
+__device__ __forceinline__ int xcd_linear(int bid, int nwg) {
+  const int xcd = bid & 7;
+  const int per = nwg >> 3;
+  const int rem = nwg & 7;
+  return (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + (bid >> 3);
+}
+
+}  // namespace sidon_flexrel
+
+// Launch of the 128-row kernel (flexrel_wide.hip) for workgroups
+// [0, nwg) of p, with p.nqb = query blocks of 128 rows per (b, h).
+namespace sidon_flexrel {
+int wide_rows();
+int wide_threads();
+hipError_t launch_wide(const Params& p, int nwg, bool same_stride, hipStream_t stream);
+}  // namespace sidon_flexrel

@@ -55,11 +55,13 @@
 #include <stdarg.h>
 #include <stdint.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <mutex>
 #include <type_traits>
 
+#include "flexrel_device.h"
 #include "sidon_flexrel.h"
 #include "sidon_host.h"
 
@@ -70,131 +72,24 @@
 
 namespace {
 
-constexpr int kD = 64;          // head dim
-constexpr int kLeft = 64;       // clamp window: j - i in [-64, 8]
-constexpr int kRight = 8;
-constexpr int kNumPos = 73;     // rows of the relative table
-constexpr int kStep = 32;       // keys per pipeline step
+using namespace sidon_flexrel;
+#define LDS_PTR SIDON_LDS_PTR
+
 constexpr int kRows = 64;       // query rows per workgroup (two 32-column blocks)
 // Key splits per workgroup: 8 wavefronts, two per SIMD (one per SIMD leaves
 // the SIMD idle on every dependency stall of its wavefront).
 constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kStages = 2;                   // ring depth (K and V) per wavefront
-constexpr int kTile = kStep * kD * 2;        // bytes of one K or V step tile
 constexpr int kWaveRing = 2 * kStages * kTile;  // K slots, then V slots
-constexpr int kQrStride = 76;                // fp32 per row of the q.rel table
 constexpr int kQrOff = kWaves * kWaveRing;
 constexpr int kQStageOff = kQrOff + kRows * kQrStride * 4;  // Q block, 64 rows x 128 B
 constexpr int kLdsBytes = kQStageOff + kRows * kD * 2;
-// A query's 32 probabilities of one step summing below 2^15 are each below
-// the fp16 maximum, so their fp16 rounding is finite; a larger (or
-// non-finite) sum sends the query through the exact max update.
-constexpr float kSumLimit = 32768.f;
 // Split merge (reuses the ring and table area after the key loop).
 constexpr int kMergeStride = 68;             // fp32 per partial-output row
 constexpr int kMergeMlOff = kWaves * kRows * kMergeStride * 4;
 static_assert(kMergeMlOff + kWaves * kRows * 2 * 4 <= kLdsBytes, "merge area too small");
 static_assert(kLdsBytes <= 160 * 1024, "LDS budget of one CU");
-
-typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-typedef short s4 __attribute__((ext_vector_type(4)));
-typedef float f2 __attribute__((ext_vector_type(2)));
-typedef float f4 __attribute__((ext_vector_type(4)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-
-#define LDS_PTR(T, p) ((__attribute__((address_space(3))) T*)(p))
-
-struct Params {
-  const _Float16* q;
-  const _Float16* k;
-  const _Float16* v;
-  const _Float16* rel;
-  const int32_t* lens;
-  _Float16* out;
-  int64_t qsb, qsh;  // batch / head strides (elements)
-  int64_t ksb, ksh;
-  int64_t vsb, vsh;
-  int64_t osb, osh;
-  int qsl, ksl, vsl, osl;  // row strides (elements, < 2^25)
-  int B, H, L;
-  int nqb;                 // query blocks per (b, h)
-  float scale;             // log2(e) / sqrt(64)
-};
-
-// 16-byte chunk c of tile row r is stored at chunk position c ^ tile_swz(r)
-// (LDS: 64 banks of 4 bytes).  The map is a bijection of row bits 1..3, which
-// keeps the 16 rows of every 16-lane ds_read_b128 group on distinct banks.
-// It puts row bit 1 on chunk bit 2: a 32-lane half of a ds_read_b64_tr_b16
-// reads rows with bits 0-1 varying and chunk bits 0-1 varying (lane bits 1
-// and 4), so row bit 1 must land on the one chunk bit that does not vary.
-__device__ __forceinline__ int tile_swz(int row) {
-  return ((row >> 2) & 1) | ((row >> 2) & 2) | ((row << 1) & 4);
-}
-
-// Key row fed to A-operand lane m of S^T = K.Q^T: bits 2 and 3 of m swapped.
-// With the 32x32 accumulator layout (lane half g holds rows 8*(i/4) + 4g +
-// i%4) element i of lane half g is then key 16*(i >> 3) + 8g + (i & 7).
-__device__ __forceinline__ int mfma_row_perm(int m) {
-  return (m & 0x13) | ((m >> 1) & 4) | ((m << 1) & 8);
-}
-
-__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
-
-// x of lane l and of lane l ^ 32 (the other half of the wavefront) combined
-// with max.  v_permlane32_swap applied to (x, x) leaves one half's
-// value in each result register, so any symmetric combination of the two is
-// the combination over the lane pair.
-__device__ __forceinline__ float pair_max(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-
-// Asynchronous copy global -> LDS of one 4 KB tile: four instructions of
-// 64 lanes x 16 bytes.  Instruction i adds 1024 i to both addresses: lane l's
-// bytes gbase[voff_i,l + 1024 i .. +16) land at LDS byte address
-// lds_addr + 1024 i + 16 l.  Issued as inline assembly so that the compiler
-// does not wait for the copy before unrelated LDS reads; completion is
-// awaited with wait_vmcnt below.  M0 is written here; nothing else in this
-// translation unit uses M0 (the clobber documents it -- the compiler treats
-// M0 as reserved).
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void dma_tile(uint32_t lds_addr, const char* gbase, uint32_t v0, uint32_t v1,
-                                         uint32_t v2, uint32_t v3) {
-  asm volatile(
-      "s_mov_b32 m0, %0\n\t"
-      "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %1, %5\n\t"
-      "global_load_lds_dwordx4 %2, %5 offset:1024\n\t"
-      "global_load_lds_dwordx4 %3, %5 offset:2048\n\t"
-      "global_load_lds_dwordx4 %4, %5 offset:3072"
-      :: "s"(lds_addr), "v"(v0), "v"(v1), "v"(v2), "v"(v3), "s"(gbase) : "memory", "m0");
-}
-__device__ __forceinline__ void dma_1k(uint32_t lds_addr, const char* gbase, uint32_t v0) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
-               :: "s"(lds_addr), "v"(v0), "s"(gbase) : "memory", "m0");
-}
-#pragma clang diagnostic pop
-
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory");
-}
-
-__device__ __forceinline__ void wait_lgkm0() {
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-}
-
-__device__ __forceinline__ void lds_barrier() {
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
-__device__ __forceinline__ h8 cat(h4 a, h4 b) {
-  return h8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
-}
 
 // kSameStride: K and V rows have the same stride (always the case for the
 // fused QKV layout), so one set of copy offsets serves both.
@@ -211,12 +106,7 @@ flexrel_fwd_kernel(const Params p) {
   // Workgroups are dispatched round-robin over the 8 XCDs; give each XCD a
   // contiguous range of (b, h, query block) so one head's K/V stays in one
   // XCD's L2.
-  const int nwg = gridDim.x;
-  const int bid = blockIdx.x;
-  const int xcd = bid & 7;
-  const int per = nwg >> 3;
-  const int rem = nwg & 7;
-  const int lin = (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + (bid >> 3);
+  const int lin = xcd_linear(blockIdx.x, gridDim.x);
   const int bh = lin / p.nqb;
   const int qblk = lin - bh * p.nqb;
   const int b = bh / p.H;
@@ -225,7 +115,7 @@ flexrel_fwd_kernel(const Params p) {
   int LK = p.L;
   if (p.lens != nullptr) LK = min(max(p.lens[b], 0), p.L);
   LK = __builtin_amdgcn_readfirstlane(LK);
-  const int q0 = qblk * kRows;
+  const int q0 = p.row0 + qblk * kRows;
   const float scale = p.scale;
 
   const _Float16* qbase = p.q + b * p.qsb + h * p.qsh;
@@ -840,16 +730,106 @@ int compute_units() {
 
 }  // namespace sidon
 
+namespace {
+
+// Kernel variants: the 64-row workgroup with 8 key splits (flexrel_fwd_kernel);
+// the 128-row wavefront with 4 key splits (flexrel_wide.hip) over all rows;
+// and the wide kernel over as many 128-row blocks as fill whole rounds of
+// the chip, the remaining rows then running on the 64-row kernel in a
+// second launch (the wide grid alone would leave its last round part-full).
+enum Variant { kSplit8 = 0, kWide = 1, kWideTail = 2 };
+
+// SIDON_FLEXREL_VARIANT=split8|wide|wide_tail forces one variant (A/B
+// timing); unset or "auto" picks by shape.
+int forced_variant() {
+  static const int v = [] {
+    const char* e = getenv("SIDON_FLEXREL_VARIANT");
+    if (e == nullptr) return -1;
+    if (strcmp(e, "split8") == 0) return (int)kSplit8;
+    if (strcmp(e, "wide") == 0) return (int)kWide;
+    if (strcmp(e, "wide_tail") == 0) return (int)kWideTail;
+    return -1;
+  }();
+  return v;
+}
+
+Variant choose_variant(int B, int H, int L, bool same_stride) {
+  if (!same_stride) return kSplit8;  // the wide kernel is built for K and V rows of one stride
+  const int f = forced_variant();
+  if (f >= 0) return (Variant)f;
+  (void)B;
+  (void)H;
+  (void)L;
+  return kSplit8;
+}
+
+// One launch: `rows` query rows per workgroup, nqb blocks per (b, h) from
+// query row row0.
+struct Launch {
+  Variant kernel;  // kSplit8 or kWide
+  int rows, splits, threads, nqb, row0;
+  long long nwg;
+};
+struct Plan {
+  int n;
+  Launch l[2];
+};
+
+Launch launch_of(Variant kernel, int B, int H, int nqb, int row0) {
+  Launch x;
+  x.kernel = kernel;
+  x.rows = kernel == kWide ? wide_rows() : kRows;
+  x.splits = kernel == kWide ? 4 : kWaves;
+  x.threads = kernel == kWide ? wide_threads() : kThreads;
+  x.nqb = nqb;
+  x.row0 = row0;
+  x.nwg = (long long)B * H * nqb;
+  return x;
+}
+
+Plan plan_of(int B, int H, int L, bool same_stride = true) {
+  Plan pl;
+  const Variant v = choose_variant(B, H, L, same_stride);
+  pl.n = 1;
+  if (v == kWideTail) {
+    const int wr = wide_rows();
+    const long long cus = sidon::compute_units();
+    const long long rounds = (long long)B * H * (L / wr) / cus;  // whole rounds of 128-row blocks
+    const int nb = (int)(rounds * cus / ((long long)B * H));      // 128-row blocks per (b, h)
+    if (nb > 0) {
+      pl.l[0] = launch_of(kWide, B, H, nb, 0);
+      const int rest = L - nb * wr;
+      if (rest > 0) {
+        pl.l[1] = launch_of(kSplit8, B, H, (rest + kRows - 1) / kRows, nb * wr);
+        pl.n = 2;
+      }
+      return pl;
+    }
+    pl.l[0] = launch_of(kSplit8, B, H, (L + kRows - 1) / kRows, 0);
+    return pl;
+  }
+  if (v == kWide) {
+    pl.l[0] = launch_of(kWide, B, H, (L + wide_rows() - 1) / wide_rows(), 0);
+  } else {
+    pl.l[0] = launch_of(kSplit8, B, H, (L + kRows - 1) / kRows, 0);
+  }
+  return pl;
+}
+
+}  // namespace
+
 SIDON_API int sidon_flexrel_launch_shape(int B, int H, int L, int* queries_per_block,
                                          int* key_splits, int* workgroups, int* threads_per_block) {
   if (B < 1 || H < 1 || L < 1) return fail(SIDON_E_SHAPE, "B=%d H=%d L=%d must be >= 1", B, H, L);
-  const long long nqb = (L + kRows - 1) / kRows;
-  const long long nwg = (long long)B * H * nqb;
-  if (nwg >= (1LL << 31)) return fail(SIDON_E_SHAPE, "grid of %lld workgroups too large", nwg);
-  if (queries_per_block) *queries_per_block = kRows;
-  if (key_splits) *key_splits = kWaves;
-  if (workgroups) *workgroups = (int)nwg;
-  if (threads_per_block) *threads_per_block = kThreads;
+  const Plan pl = plan_of(B, H, L);
+  long long total = 0;
+  for (int i = 0; i < pl.n; ++i) total += pl.l[i].nwg;
+  if (total >= (1LL << 31)) return fail(SIDON_E_SHAPE, "grid of %lld workgroups too large", total);
+  // The first launch's shape; workgroups counts every launch of the call.
+  if (queries_per_block) *queries_per_block = pl.l[0].rows;
+  if (key_splits) *key_splits = pl.l[0].splits;
+  if (workgroups) *workgroups = (int)total;
+  if (threads_per_block) *threads_per_block = pl.l[0].threads;
   return SIDON_OK;
 }
 
@@ -868,8 +848,7 @@ SIDON_API int sidon_flexrel_fwd(const void* q, const void* k, const void* v, con
     return rc;
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(rel) || !aligned16(out))
     return fail(SIDON_E_ALIGN, "q, k, v, rel and out must be 16-byte aligned");
-  int wg_threads = 0, nwg = 0, nq = 0, nk = 0;
-  if ((rc = sidon_flexrel_launch_shape(B, H, L, &nq, &nk, &nwg, &wg_threads))) return rc;
+  if ((rc = sidon_flexrel_launch_shape(B, H, L, nullptr, nullptr, nullptr, nullptr))) return rc;
   if ((rc = check_device())) return rc;
 
   Params p;
@@ -894,15 +873,25 @@ SIDON_API int sidon_flexrel_fwd(const void* q, const void* k, const void* v, con
   p.B = B;
   p.H = H;
   p.L = L;
-  p.nqb = (L + kRows - 1) / kRows;
   p.scale = 1.4426950408889634f / 8.0f;  // log2(e) / sqrt(64)
 
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  if (p.ksl == p.vsl)
-    hipLaunchKernelGGL(flexrel_fwd_kernel<true>, dim3(nwg), dim3(kThreads), 0, s, p);
-  else
-    hipLaunchKernelGGL(flexrel_fwd_kernel<false>, dim3(nwg), dim3(kThreads), 0, s, p);
-  const hipError_t err = hipGetLastError();
+  const Plan pl = plan_of(B, H, L, p.ksl == p.vsl);
+  hipError_t err = hipSuccess;
+  for (int i = 0; i < pl.n && err == hipSuccess; ++i) {
+    const Launch& x = pl.l[i];
+    p.nqb = x.nqb;
+    p.row0 = x.row0;
+    if (x.kernel == kWide) {
+      err = launch_wide(p, (int)x.nwg, true, s);
+    } else {
+      if (p.ksl == p.vsl)
+        hipLaunchKernelGGL(flexrel_fwd_kernel<true>, dim3((unsigned)x.nwg), dim3(kThreads), 0, s, p);
+      else
+        hipLaunchKernelGGL(flexrel_fwd_kernel<false>, dim3((unsigned)x.nwg), dim3(kThreads), 0, s, p);
+      err = hipGetLastError();
+    }
+  }
   if (err != hipSuccess) return fail(SIDON_E_LAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
   return SIDON_OK;
 }
