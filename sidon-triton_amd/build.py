@@ -47,8 +47,21 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (set HIPCC or install ROCm)")
 
 
+def generate(verbose: bool = False) -> None:
+    """Writes csrc/flexrel_wide_step.inc (the hand-scheduled key-step loop of
+    flexrel_wide.hip) from csrc/gen_wide_step.py, which also checks its wait
+    states and load accounting."""
+    gen = PKG_DIR / "csrc" / "gen_wide_step.py"
+    proc = subprocess.run([sys.executable, str(gen)], capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"{gen.name} failed ({proc.returncode}):\n{proc.stdout}{proc.stderr}")
+    if verbose:
+        print(proc.stderr.strip(), flush=True)
+
+
 def build(verbose: bool = False) -> Path:
     """Compile the HIP library; returns its path.  Raises on a compile error."""
+    generate(verbose)
     out = PKG_DIR / LIB_NAME
     tmp = out.with_name(out.name + f".tmp{os.getpid()}")
     cmd = [hipcc(), *HIP_FLAGS, f"-I{REPO_DIR / 'include'}", "-o", str(tmp), *map(str, SOURCES), *LIBS]

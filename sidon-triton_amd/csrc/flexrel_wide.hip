@@ -38,6 +38,7 @@
 #include <type_traits>
 
 #include "flexrel_device.h"
+#include "flexrel_wide_step.inc"
 
 #define SIDON_INLINE __attribute__((always_inline))
 
@@ -285,13 +286,19 @@ flexrel_wide_kernel(const Params p) {
     oacc[J][0] = f32x16{};
     oacc[J][1] = f32x16{};
   }
-  float m_run[kBlocks], l_run[kBlocks];
+  float m_run[kBlocks];
+  // Running row sums per block, accumulated on the matrix core (see rowsum
+  // below): the four values of a lane are its query's sum.
+  f32x4 lsum[kBlocks];
 #pragma unroll
   for (int J = 0; J < kBlocks; ++J) {
     m_run[J] = -INFINITY;
-    l_run[J] = 0.f;
+    lsum[J] = f32x4{};
   }
-  f32x16 sacc[2];        // S^T of items i (buffer i & 1) and i + 1
+  // S^T of items i (buffer i & 1) and i + 1.  Zeroed: every value bound to
+  // a register of the key-step loop must be defined at its entry, or the
+  // compiler may place other inputs in that register.
+  f32x16 sacc[2] = {};
   h8 pk[2][2] = {};      // fp16 probabilities [buffer][16-key half]
   h8 kop[4];             // K operands (16 dims per k-step) of one step
   h8 vop[2][2];          // V^T operands [hh][db] of one step
@@ -374,6 +381,13 @@ flexrel_wide_kernel(const Params p) {
     rs = __builtin_amdgcn_mfma_f32_16x16x32_f16(sel, pk[bf][0], f32x4{}, 0, 0, 0);
     rs = __builtin_amdgcn_mfma_f32_16x16x32_f16(sel, pk[bf][1], rs, 0, 0, 0);
   };
+  // The same row sums added to block J's running sums (the hand-scheduled
+  // plain step issues exactly these two products per item).
+  auto accumulate = [&](int J, int bf) SIDON_INLINE {
+    asm volatile("" : "+v"(sel));
+    lsum[J] = __builtin_amdgcn_mfma_f32_16x16x32_f16(sel, pk[bf][0], lsum[J], 0, 0, 0);
+    lsum[J] = __builtin_amdgcn_mfma_f32_16x16x32_f16(sel, pk[bf][1], lsum[J], 0, 0, 0);
+  };
 
   auto emit = [&](int bf, int i, const f2& e) SIDON_INLINE {
     const h2 ph = __builtin_convertvector(e, h2);
@@ -441,12 +455,14 @@ flexrel_wide_kernel(const Params p) {
       }
     };
     // Recompute with the running max; then raise the max of the queries that
-    // need it: all at the first step (the max is -inf), else those whose step
-    // sum left the fp16-safe range.  Per query, never per wavefront, so one
-    // row cannot change the rounding of another -- and the sum that decides
-    // is the query's own: the matrix-core row sum also multiplies the other
-    // query of the lane group by 0, and 0 * inf = NaN, so an overflowing
-    // neighbour (a garbage padded row, say) would read as an overflow here.
+    // need it: all at the first step (the max is -inf), else those with a
+    // probability past the fp16 range (inf, so a non-finite step sum; every
+    // finite fp16 probability is safe: the sums and products are fp32).  Per
+    // query, never per wavefront, so one row cannot change the rounding of
+    // another -- and the sum that decides is the query's own: the
+    // matrix-core row sum also multiplies the other query of the lane group
+    // by 0, and 0 * inf = NaN, so an overflowing neighbour (a garbage padded
+    // row, say) would read as an overflow there.
     if (!first) probs(m_run[J]);
     if (first || need_sum) {
       bool need = first;
@@ -457,7 +473,7 @@ flexrel_wide_kernel(const Params p) {
 #pragma unroll
           for (int e = 0; e < 8; ++e) own += (float)pk[bf][hh][e];
         const auto pr = __builtin_amdgcn_permlane32_swap(__float_as_uint(own), __float_as_uint(own), false, false);
-        need = !(__uint_as_float(pr[0]) + __uint_as_float(pr[1]) < kSumLimit);
+        need = !(__uint_as_float(pr[0]) + __uint_as_float(pr[1]) < INFINITY);
       }
       float mx = y[0];
 #pragma unroll
@@ -470,7 +486,7 @@ flexrel_wide_kernel(const Params p) {
         oacc[J][0] *= alpha;
         oacc[J][1] *= alpha;
       }
-      l_run[J] *= alpha;
+      lsum[J] *= alpha;
       m_run[J] = m_new;
       probs(m_new);
     }
@@ -478,14 +494,13 @@ flexrel_wide_kernel(const Params p) {
   };
   // Deferred check of item (u, J) (buffer bf; its row sums were issued one
   // phase ago, its probabilities are consumed by the next PV product): a
-  // step sum outside the fp16-safe range sends the block through the max
-  // update (which decides per query from the query's own sum and leaves
-  // every probability finite, so the recomputed row sums are exact).  Then
-  // the step sums join the running sums.
+  // non-finite step sum sends the block through the max update (which
+  // decides per query from the query's own sum and leaves every probability
+  // finite).  Then the item's row sums join the running sums.
   auto settle = [&](int u, int J, int bf) SIDON_INLINE {
     asm volatile("" : "+v"(rs));
-    if (__builtin_expect(__builtin_amdgcn_ballot_w64(!(rs[0] < kSumLimit)) != 0, 0)) general(u, J, bf, false, true);
-    l_run[J] += rs[0];
+    if (__builtin_expect(__builtin_amdgcn_ballot_w64(!(rs[0] < INFINITY)) != 0, 0)) general(u, J, bf, false, true);
+    accumulate(J, bf);
   };
 
   if (active) {
@@ -493,88 +508,61 @@ flexrel_wide_kernel(const Params p) {
     load_k(0);
     load_v(0);        // finite operands for the zero probabilities of items -2 and -1
     qk(0, 0);         // S^T of item (0, 0)
-    uint64_t overflow = 0;  // fast steps: lanes whose step sum left the fp16-safe range
-    // One processed step (index j, local step u = u_of(j), 32 keys).  kFast:
-    // a plain step (every block entirely left or entirely right of the
-    // window, not straddling LK, not the first processed step), so no item
-    // needs the general form.
-    auto step = [&](int j, auto fast_tag) SIDON_INLINE {
-      constexpr bool kFast = decltype(fast_tag)::value;
-      const int u = kFast ? plain_u(j) : u_of(j);
-      // (j = 0: item i - 1 does not exist and rs is 0; the first fast step's
-      // predecessor may be a special step)
-      const int u_prev = (kFast && j > nS) ? plain_u(j - 1) : u_of(max(j - 1, 0));
+    // One step through the general code (index j, local step u = u_of(j),
+    // 32 keys): every item whose block is not plain (band, straddling LK, or
+    // the wavefront's first step) takes the general form.
+    auto step = [&](int j) SIDON_INLINE {
+      const int u = u_of(j);
+      const int u_prev = u_of(max(j - 1, 0));  // (j = 0: item i - 1 does not exist and rs is 0)
       const int sl = j & 1;  // ring slot of this step's K and V
-      const bool all_left = u <= uL[0];
       // Phase J: item i = 4 j + J in buffer J & 1.
 #pragma unroll
       for (int J = 0; J < kBlocks; ++J) {
         const int bf = J & 1;
         const int Jm2 = (J + 2) & 3, Jm1 = (J + 3) & 3, Jp1 = (J + 1) & 3;
-        const bool is_left = kFast ? all_left : u <= uL[J];
-        const bool plain = kFast || (j > 0 && (is_left || u >= uR[J]) && u < uM);
+        const bool is_left = u <= uL[J];
+        const bool plain = j > 0 && (is_left || u >= uR[J]) && u < uM;
         const float nb = (is_left ? qr_l[J] : qr_r[J]) - m_run[J];
         if (J == 1) wait_vmcnt<12>();  // V(j) landed
         if (J == 2) wait_vmcnt<8>();   // K(j + 1) landed
         pv(Jm2, bf);  // item i - 2 (its buffer is this item's)
         probs_fast(bf, nb, 0);
         asm volatile("" : "+v"(pk[bf][0]));
-        if (kFast) {
-          // One PV MFMA, then five VALU instructions of the softmax, so the
-          // matrix core and the vector ALU work side by side.
-#pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
-          }
-        }
-        if (kFast) {
-          // Item i - 1: record an overflow (handled by the rerun below) and
-          // add the step sums -- no branch.
-          asm volatile("" : "+v"(rs));
-          overflow |= __builtin_amdgcn_ballot_w64(!(rs[0] < kSumLimit));
-          l_run[Jm1] += rs[0];
-        } else {
-          settle(J == 0 ? u_prev : u, Jm1, bf ^ 1);  // item i - 1 (J == 0: the previous step's block 3)
-        }
+        settle(J == 0 ? u_prev : u, Jm1, bf ^ 1);  // item i - 1 (J == 0: the previous step's block 3)
         qk(Jp1, bf ^ 1);      // item i + 1 (J == 3: the next step's block 0, K operands loaded in phase 2)
         if (J == 0) {
           wait_lgkm0();  // the K(j) operand reads are done: refill slot sl with K(j + 2)
-          copy_step(kbase, kstride, koff, koff_last, j + 2, ring_lds + sl * kTile, fast_tag);
+          copy_step(kbase, kstride, koff, koff_last, j + 2, ring_lds + sl * kTile, std::false_type{});
         }
         if (J == 2) {
           wait_lgkm0();  // the V(j) operand reads are done: refill slot sl with V(j + 2)
-          copy_step(vbase, vstride, voff, voff_last, j + 2, ring_lds + kVRing + sl * kTile, fast_tag);
+          copy_step(vbase, vstride, voff, voff_last, j + 2, ring_lds + kVRing + sl * kTile, std::false_type{});
         }
         if (J == 1) load_v(sl);      // V operands of step j (after the PV of item (j - 1, 3))
         if (J == 2) load_k(sl ^ 1);  // K operands of step j + 1 (after the QK of item (j, 3))
         probs_fast(bf, nb, 1);
         rowsum(bf);
         asm volatile("" : "+v"(pk[bf][0]), "+v"(pk[bf][1]));
-        if (!kFast && __builtin_expect(!plain, 0)) general(u, J, bf, j == 0, false);
-        if (kFast) {
-          // The score product's 4 dependent MFMAs each next to five VALU
-          // instructions (none waits on its predecessor), then the row sums;
-          // nothing of the next phase moves into this one.
-#pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
-          }
-          __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-          __builtin_amdgcn_sched_barrier(0);
-        }
+        if (__builtin_expect(!plain, 0)) general(u, J, bf, j == 0, false);
       }
     };
-    // The plain steps run optimistically: an item whose probabilities left
-    // the fp16-safe range (rare: a score more than ~10 log2 units above the
-    // running max) only sets `overflow`; the wavefront then discards its
-    // partial results and runs all its steps again through the general form,
-    // which rescales per query exactly where needed -- and computes the same
-    // values as the fast form for every query that does not overflow.
+
+    // The first pass runs every step through the hand-scheduled loop of
+    // flexrel_wide_step.inc: the special steps (band, straddling LK, the
+    // first) with exactly the general code's arithmetic per item, then the
+    // plain steps ordered for one wavefront per SIMD -- which issues a vector
+    // instruction about every 5.4 cycles (v_exp_f32: 9.1) while a 32x32x16
+    // product holds the matrix core for 32, so the two must run side by
+    // side.  It checks no step sum: a probability past the fp16 range becomes
+    // inf and makes its block's running sum non-finite (inf, or NaN through
+    // the other query's zero weight).  Such a wavefront discards its partial
+    // results and runs all its steps again through the C++ general code,
+    // which raises the running max exactly where needed and computes the
+    // same values as the first pass for every query whose probabilities stay
+    // finite.
     for (bool safe = false;; safe = true) {
       if (safe) {
-        wait_vmcnt<0>();  // the fast loop's last prefetches have landed
+        wait_vmcnt<0>();  // the last prefetches have landed
         wait_lgkm0();
         copy_step(kbase, kstride, koff, koff_last, 0, ring_lds, std::false_type{});
         copy_step(vbase, vstride, voff, voff_last, 0, ring_lds + kVRing, std::false_type{});
@@ -585,7 +573,7 @@ flexrel_wide_kernel(const Params p) {
           oacc[J][0] = f32x16{};
           oacc[J][1] = f32x16{};
           m_run[J] = -INFINITY;
-          l_run[J] = 0.f;
+          lsum[J] = f32x4{};
         }
         pk[0][0] = pk[0][1] = pk[1][0] = pk[1][1] = h8{};
         rs = f32x4{};
@@ -593,19 +581,65 @@ flexrel_wide_kernel(const Params p) {
         load_k(0);
         load_v(0);
         qk(0, 0);
-      }
-      int j = 0;
-      const int n_slow = safe ? nu : nSlow;
-      for (; j < n_slow; ++j) step(j, std::false_type{});
-      for (; j < nu; ++j) step(j, std::true_type{});
-      if (n_slow < nu) {  // the last item was a fast one
-        asm volatile("" : "+v"(rs));
-        overflow |= __builtin_amdgcn_ballot_w64(!(rs[0] < kSumLimit));
-        l_run[3] += rs[0];
-        if (__builtin_expect(overflow != 0, 0)) continue;
-      } else {
+        for (int j = 0; j < nu; ++j) step(j);
         settle(u_of(nu - 1), 3, 1);
+        break;
       }
+      // Loop state: j, the copy bases and their advances for the plain
+      // steps (by 4 key steps, or across the band at index jump), the
+      // scalars of the processing order, and the per-lane LDS addresses of
+      // the operand reads (slot 0) and of the lane's q.rel row.
+      int jreg = 0;
+      const int jump = nS + cL;
+      const int64_t dstep = (int64_t)(kWaves * kStep) * kstride;
+      const int64_t djump = dstep * (1 + cR - cL);
+      const char* gk = kbase;
+      const char* gv = vbase;
+      const uint64_t kb = (uint64_t)(uintptr_t)(kbase - 3072), vb = (uint64_t)(uintptr_t)(vbase - 3072);
+      const uint32_t rowb = (uint32_t)(kStep * kstride);
+      const int tlast = ragged ? T - 1 : -1;
+      uint32_t ka[4], tv[2][2];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) ka[s] = (uint32_t)(uintptr_t)SIDON_LDS_PTR(char, kaddr[0][s]);
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+        for (int db = 0; db < 2; ++db) tv[hf][db] = ring_lds + (uint32_t)tr_off[hf][db];
+      const uint32_t qbase = (uint32_t)(uintptr_t)SIDON_LDS_PTR(float, qr_tab + n * kQrStride);
+      const int laned = 8 * g - n;
+      const int g8 = 8 * g;
+      asm volatile(SIDON_WIDE_LOOP
+                   : "+{v[0:15]}"(oacc[0][0]), "+{v[16:31]}"(oacc[0][1]), "+{v[32:47]}"(oacc[1][0]),
+                     "+{v[48:63]}"(oacc[1][1]), "+{v[64:79]}"(oacc[2][0]), "+{v[80:95]}"(oacc[2][1]),
+                     "+{v[96:111]}"(oacc[3][0]), "+{v[112:127]}"(oacc[3][1]), "+{v[128:143]}"(sacc[0]),
+                     "+{v[144:159]}"(sacc[1]), "+{v[160:163]}"(pk[0][0]), "+{v[164:167]}"(pk[0][1]),
+                     "+{v[168:171]}"(pk[1][0]), "+{v[172:175]}"(pk[1][1]), "+{v[176:179]}"(lsum[0]),
+                     "+{v[180:183]}"(lsum[1]), "+{v[184:187]}"(lsum[2]), "+{v[188:191]}"(lsum[3]),
+                     "+{v[192:195]}"(sel), "+{a[0:3]}"(qop[0][0]), "+{a[4:7]}"(qop[0][1]), "+{a[8:11]}"(qop[0][2]),
+                     "+{a[12:15]}"(qop[0][3]), "+{a[16:19]}"(qop[1][0]), "+{a[20:23]}"(qop[1][1]),
+                     "+{a[24:27]}"(qop[1][2]), "+{a[28:31]}"(qop[1][3]), "+{a[32:35]}"(qop[2][0]),
+                     "+{a[36:39]}"(qop[2][1]), "+{a[40:43]}"(qop[2][2]), "+{a[44:47]}"(qop[2][3]),
+                     "+{a[48:51]}"(qop[3][0]), "+{a[52:55]}"(qop[3][1]), "+{a[56:59]}"(qop[3][2]),
+                     "+{a[60:63]}"(qop[3][3]), "+{a[64:67]}"(kop[0]), "+{a[68:71]}"(kop[1]), "+{a[72:75]}"(kop[2]),
+                     "+{a[76:79]}"(kop[3]), "+{a[80:83]}"(vop[0][0]), "+{a[84:87]}"(vop[0][1]),
+                     "+{a[88:91]}"(vop[1][0]), "+{a[92:95]}"(vop[1][1]), "+{s64}"(jreg), "+{s[70:71]}"(gk),
+                     "+{s[72:73]}"(gv), [m0] "+v"(m_run[0]), [m1] "+v"(m_run[1]), [m2] "+v"(m_run[2]),
+                     [m3] "+v"(m_run[3])
+                   : "{s65}"(nu), "{s66}"(jump), "{s67}"(ring_lds), "{s68}"(scale), "{s[74:75]}"(dstep),
+                     "{s[76:77]}"(djump), [nslow] "s"(nSlow), [w] "s"(w), [q0] "s"(q0), [lk] "s"(LK),
+                     [tlast] "s"(tlast), [cl] "s"(cL), [nband] "s"(cR - cL), [ns] "s"(nS), [ue] "s"(uE),
+                     [rowb] "s"(rowb), [kblo] "s"((uint32_t)kb), [kbhi] "s"((uint32_t)(kb >> 32)),
+                     [vblo] "s"((uint32_t)vb), [vbhi] "s"((uint32_t)(vb >> 32)), [ko0] "v"(koff[0]),
+                     [ko1] "v"(koff[1]), [ko2] "v"(koff[2]), [ko3] "v"(koff[3]), [kl0] "v"(koff_last[0]),
+                     [kl1] "v"(koff_last[1]), [kl2] "v"(koff_last[2]), [kl3] "v"(koff_last[3]), [ka0] "v"(ka[0]),
+                     [ka1] "v"(ka[1]), [ka2] "v"(ka[2]), [ka3] "v"(ka[3]), [tv00] "v"(tv[0][0]),
+                     [tv01] "v"(tv[0][1]), [tv10] "v"(tv[1][0]), [tv11] "v"(tv[1][1]), [qbase] "v"(qbase),
+                     [laned] "v"(laned), [g8] "v"(g8)
+                   : SIDON_WIDE_VGPR_CLOBBERS, SIDON_WIDE_SGPR_CLOBBERS, "vcc", "m0", "scc", "memory");
+      uint64_t overflow = 0;
+#pragma unroll
+      for (int J = 0; J < kBlocks; ++J) overflow |= __builtin_amdgcn_ballot_w64(!(lsum[J][0] < INFINITY));
+      if (__builtin_expect(overflow != 0, 0)) continue;
       break;
     }
     wait_lgkm0();
@@ -631,7 +665,7 @@ flexrel_wide_kernel(const Params p) {
     }
     if (g == 0) {
       ml[(w * kRows + 32 * J + n) * 2] = m_run[J];
-      ml[(w * kRows + 32 * J + n) * 2 + 1] = l_run[J];
+      ml[(w * kRows + 32 * J + n) * 2 + 1] = lsum[J][0];
     }
   }
   lds_barrier();
@@ -643,20 +677,20 @@ flexrel_wide_kernel(const Params p) {
   float mmax = -INFINITY;
 #pragma unroll
   for (int s = 0; s < kWaves; ++s) mmax = fmaxf(mmax, ml[(s * kRows + r) * 2]);
-  float lsum = 0.f;
+  float total = 0.f;
   f4 o[8] = {};
 #pragma unroll
   for (int s = 0; s < kWaves; ++s) {
     const float ms = ml[(s * kRows + r) * 2];
     const float f = ms == -INFINITY ? 0.f : fast_exp2(ms - mmax);
-    lsum += ml[(s * kRows + r) * 2 + 1] * f;
+    total += ml[(s * kRows + r) * 2 + 1] * f;
     const float* src = mo + (s * kRows + r) * kMergeStride + c;
 #pragma unroll
     for (int j = 0; j < 8; ++j) o[j] += *reinterpret_cast<const f4*>(src + 4 * j) * f;
   }
   const int row = q0 + r;
   if (row < p.L) {
-    const float inv = lsum > 0.f ? __builtin_amdgcn_rcpf(lsum) : 0.f;
+    const float inv = total > 0.f ? __builtin_amdgcn_rcpf(total) : 0.f;
     _Float16* dst = p.out + b * p.osb + h * p.osh + (int64_t)row * p.osl + c;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {

@@ -1,0 +1,134 @@
+"""The hand-scheduled key-step loop of flexrel_wide.hip (CPU only).
+
+* The generator's checks (csrc/gen_wide_step.py) pass on the loop it writes,
+  and they catch planted mistakes: a removed wait state, a missing LDS wait.
+* Operand placement in the compiled kernel: the loop's text names fixed
+  registers (v0-v220, a0-a95, s64-s95); every register the compiler
+  substituted for a named operand must lie outside them.  (An operand bound
+  to a fixed register whose value is undefined at the loop entry lets the
+  compiler place other inputs inside it -- a mistake this test catches.)
+"""
+
+from __future__ import annotations
+
+import importlib.util
+import re
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+import pytest
+
+REPO = Path(__file__).resolve().parents[1]
+CSRC = REPO / "sidon-triton_amd" / "csrc"
+
+
+def _gen():
+    spec = importlib.util.spec_from_file_location("gen_wide_step", CSRC / "gen_wide_step.py")
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def test_generator_checks_pass():
+    gen = _gen()
+    loop, step, cycles = gen.build()
+    assert len(step) > 200 and 1000 < cycles < 2000
+    kinds = [i.kind for i in step]
+    assert kinds.count("mfma") == 40 and kinds.count("trans") == 64
+
+
+def test_hazard_check_catches_a_removed_wait_state():
+    gen = _gen()
+    _, step, _ = gen.build()
+    seq = gen.FENCE + step
+    # plant: drop the wait states between a probability conversion and the
+    # row-sum product reading it by moving the product right after it
+    i = next(k for k, ins in enumerate(seq) if ins.text.startswith("v_mfma_f32_16x16x32_f16"))
+    cvt = next(k for k, ins in enumerate(seq) if ins.text.startswith("v_cvt_pk_f16_f32"))
+    reader = next(k for k in range(cvt + 1, len(seq)) if seq[k].kind == "mfma" and seq[k].reads & seq[cvt].writes)
+    planted = seq[:cvt + 1] + [seq[reader]] + seq[cvt + 1:reader] + seq[reader + 1:]
+    with pytest.raises(AssertionError, match="hazard"):
+        gen.check_hazards(planted)
+    gen.check_hazards(seq)
+    del i
+
+
+def test_wait_check_catches_a_missing_lds_wait():
+    gen = _gen()
+    _, step, _ = gen.build()
+    # plant: drop the lgkmcnt wait before the score product that reads the
+    # freshly loaded K operands
+    waits = [k for k, ins in enumerate(step) if ins.text == "s_waitcnt lgkmcnt(0)"]
+    planted = step[:waits[-1]] + step[waits[-1] + 1:]
+    first = 0
+    with pytest.raises(AssertionError):
+        gen.check_waits(planted + step, [("K", first), ("V", first), ("K", 1), ("V", 1)])
+
+
+def _compiled_loop():
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(hipcc).exists():
+        pytest.skip("hipcc not available")
+    sys.path.insert(0, str(REPO / "sidon-triton_amd"))
+    try:
+        import build as sidon_build
+    finally:
+        sys.path.pop(0)
+    sidon_build.generate()
+    flags = [f for f in sidon_build.HIP_FLAGS if f not in ("-fPIC", "-shared")]
+    out = subprocess.run([hipcc, *flags, "--cuda-device-only", "-S", "-o", "-", f"-I{REPO / 'include'}",
+                          str(CSRC / "flexrel_wide.hip")], capture_output=True, text=True, timeout=600)
+    assert out.returncode == 0, out.stderr[-2000:]
+    asm = out.stdout
+    blocks = re.findall(r";;#ASMSTART\n(.*?);;#ASMEND", asm, re.S)
+    loop = [b for b in blocks if "L_sp_top_" in b]
+    assert len(loop) == 1
+    return [ln.strip() for ln in loop[0].splitlines() if ln.strip()]
+
+
+def _template():
+    text = (CSRC / "flexrel_wide_step.inc").read_text()
+    body = text.split("#define SIDON_WIDE_LOOP \\\n", 1)[1]
+    return [m.group(1).strip() for m in re.finditer(r'"(.*?)\\n\\t"', body)]
+
+
+def _reg_set(tok):
+    m = re.fullmatch(r"([vsa])(\d+)", tok) or re.fullmatch(r"([vsa])\[(\d+):(\d+)\]", tok)
+    assert m, tok
+    lo = int(m.group(2))
+    hi = int(m.group(3)) if m.lastindex == 3 else lo
+    return {(m.group(1), r) for r in range(lo, hi + 1)}
+
+
+def test_compiled_operands_avoid_the_loop_registers():
+    compiled = _compiled_loop()
+    template = [ln for ln in _template()]
+    assert len(compiled) == len(template)
+    bound = {}
+    for tpl, got in zip(template, compiled):
+        if "%[" not in tpl:
+            continue
+        # split both lines into tokens and pair the placeholders
+        tt = re.split(r"[\s,]+", tpl.replace("%=", "0"))
+        gt = re.split(r"[\s,]+", got)
+        assert len(tt) == len(gt), (tpl, got)
+        for a, b in zip(tt, gt):
+            if a.startswith("%["):
+                name = a[2:a.index("]")]
+                bound.setdefault(name, set()).add(b)
+    reserved = ({("v", r) for r in range(0, 221)} | {("a", r) for r in range(0, 96)}
+                | {("s", r) for r in range(64, 96)})
+    seen = {}
+    for name, regs in bound.items():
+        assert len(regs) == 1, (name, regs)   # one register per operand throughout the loop
+        reg = next(iter(regs))
+        rs = _reg_set(reg)
+        assert not (rs & reserved), (name, reg)
+        for other, ors in seen.items():
+            assert not (rs & ors), (name, reg, other)
+        seen[name] = rs
+    # every input the loop reads is bound
+    for name in ("qbase", "laned", "g8", "ka0", "tv00", "ko0", "kl0", "m0", "nslow", "w", "q0", "lk"):
+        assert name in bound, name
