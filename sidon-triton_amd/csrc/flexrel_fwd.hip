@@ -753,14 +753,20 @@ int forced_variant() {
   return v;
 }
 
+// Automatic choice, from launch timings on MI355X (H = 16, L = 500 .. 4800):
+// the 128-row kernel wins once its blocks fill more than about half of the
+// chip's compute units (its per-workgroup prologue and merge cost more than
+// the 64-row kernel's, its steps less); past one full round, the rows of the
+// part-full last round go to the 64-row kernel.
 Variant choose_variant(int B, int H, int L, bool same_stride) {
   if (!same_stride) return kSplit8;  // the wide kernel is built for K and V rows of one stride
   const int f = forced_variant();
   if (f >= 0) return (Variant)f;
-  (void)B;
-  (void)H;
-  (void)L;
-  return kSplit8;
+  const long long blocks = (long long)B * H * ((L + wide_rows() - 1) / wide_rows());
+  const long long cus = sidon::compute_units();
+  if (blocks * 20 < cus * 11) return kSplit8;
+  if (blocks <= cus) return kWide;
+  return kWideTail;
 }
 
 // One launch: `rows` query rows per workgroup, nqb blocks per (b, h) from

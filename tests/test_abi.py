@@ -47,11 +47,32 @@ def test_version(sidon):
 
 @pytest.mark.parametrize("B,H,L", [(1, 16, 4800), (1, 16, 750), (1, 16, 1500), (4, 16, 100), (1, 1, 1)])
 def test_launch_shape(sidon, B, H, L):
+    """Workgroups of all launches: one per block of the first launch's rows,
+    or, when whole rounds of 128-row blocks are followed by 64-row blocks for
+    the remaining rows, between the counts of the two block sizes."""
     s = sidon._lib.launch_shape(B, H, L)
     qpb = s["queries_per_block"]
-    assert s["workgroups"] == B * H * -(-L // qpb)
+    wgs = s["workgroups"]
+    assert qpb in (64, 128)
+    if qpb == 64:
+        assert wgs == B * H * -(-L // 64)
+    else:
+        assert B * H * -(-L // 128) <= wgs <= B * H * -(-L // 64)
     assert s["threads_per_block"] % 64 == 0
     assert s["key_splits"] >= 1
+
+
+def test_shape_choice(sidon):
+    """Without a device the library assumes 256 compute units: c3 (608
+    blocks of 128 rows) runs two whole rounds on the 128-row kernel and the
+    last 704 rows as 64-row blocks; c2 (192 blocks) the 128-row kernel; c1
+    (96 blocks, under half the chip) the 64-row kernel."""
+    c3 = sidon._lib.launch_shape(1, 16, 4800)
+    assert c3["queries_per_block"] == 128 and c3["workgroups"] == 512 + 16 * 11
+    c2 = sidon._lib.launch_shape(1, 16, 1500)
+    assert c2["queries_per_block"] == 128 and c2["workgroups"] == 16 * 12
+    c1 = sidon._lib.launch_shape(1, 16, 750)
+    assert c1["queries_per_block"] == 64 and c1["workgroups"] == 16 * 12
 
 
 def _fwd(lib, **over):
