@@ -18,7 +18,7 @@ PKG_DIR = Path(__file__).resolve().parent
 REPO_DIR = PKG_DIR.parent
 LIB_NAME = "libsidon_flexrel.so"
 SOURCES = [PKG_DIR / "csrc" / name
-           for name in ("flexrel_fwd.hip", "flexrel_wide.hip", "res_norm.hip", "conformer_ops.hip", "fbank.hip", "gemm.hip", "blas.hip")]
+           for name in ("flexrel_fwd.hip", "flexrel_wide.hip", "flexrel_w64.hip", "res_norm.hip", "conformer_ops.hip", "fbank.hip", "gemm.hip", "blas.hip")]
 # rocBLAS for the plain GEMMs of csrc/blas.hip.  Its soname is the one torch
 # bundles, so inside a torch process the library shares torch's copy.
 LIBS = ["-lrocblas"]
@@ -51,12 +51,13 @@ def generate(verbose: bool = False) -> None:
     """Writes csrc/flexrel_wide_step.inc (the hand-scheduled key-step loop of
     flexrel_wide.hip) from csrc/gen_wide_step.py, which also checks its wait
     states and load accounting."""
-    gen = PKG_DIR / "csrc" / "gen_wide_step.py"
-    proc = subprocess.run([sys.executable, str(gen)], capture_output=True, text=True)
-    if proc.returncode != 0:
-        raise RuntimeError(f"{gen.name} failed ({proc.returncode}):\n{proc.stdout}{proc.stderr}")
-    if verbose:
-        print(proc.stderr.strip(), flush=True)
+    for name in ("gen_wide_step.py", "gen_w64_step.py"):
+        gen = PKG_DIR / "csrc" / name
+        proc = subprocess.run([sys.executable, str(gen)], capture_output=True, text=True)
+        if proc.returncode != 0:
+            raise RuntimeError(f"{gen.name} failed ({proc.returncode}):\n{proc.stdout}{proc.stderr}")
+        if verbose:
+            print(proc.stderr.strip(), flush=True)
 
 
 def build(verbose: bool = False) -> Path:

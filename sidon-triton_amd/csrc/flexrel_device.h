@@ -140,4 +140,9 @@ namespace sidon_flexrel {
 int wide_rows();
 int wide_threads();
 hipError_t launch_wide(const Params& p, int nwg, bool same_stride, hipStream_t stream);
+// Launch of the 64-row, two-workgroups-per-CU kernel (flexrel_w64.hip), with
+// p.nqb = query blocks of 64 rows per (b, h).
+int w64_rows();
+int w64_threads();
+hipError_t launch_w64(const Params& p, int nwg, bool same_stride, hipStream_t stream);
 }  // namespace sidon_flexrel

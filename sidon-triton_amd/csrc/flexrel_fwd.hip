@@ -732,47 +732,47 @@ int compute_units() {
 
 namespace {
 
-// Kernel variants: the 64-row workgroup with 8 key splits (flexrel_fwd_kernel);
-// the 128-row wavefront with 4 key splits (flexrel_wide.hip) over all rows;
-// and the wide kernel over as many 128-row blocks as fill whole rounds of
-// the chip, the remaining rows then running on the 64-row kernel in a
-// second launch (the wide grid alone would leave its last round part-full).
-enum Variant { kSplit8 = 0, kWide = 1, kWideTail = 2 };
+// Kernel variants: the 64-row workgroup with 8 key splits and one workgroup
+// per compute unit (flexrel_fwd_kernel, any K / V strides); the 64-row
+// workgroup with 4 key splits and two workgroups per compute unit
+// (flexrel_w64.hip); the 128-row wavefront with 4 key splits (flexrel_wide.hip)
+// over all rows; and the wide kernel over as many 128-row blocks as fill
+// whole rounds of the chip, the remaining rows then running on the 8-split
+// kernel in a second launch.
+enum Variant { kSplit8 = 0, kWide = 1, kWideTail = 2, kW64 = 3 };
 
-// SIDON_FLEXREL_VARIANT=split8|wide|wide_tail forces one variant (A/B
-// timing); unset or "auto" picks by shape.
+// SIDON_FLEXREL_VARIANT=split8|wide|wide_tail|w64 forces one variant (A/B
+// timing and tests; read at every call); unset or "auto" picks by shape.
 int forced_variant() {
-  static const int v = [] {
-    const char* e = getenv("SIDON_FLEXREL_VARIANT");
-    if (e == nullptr) return -1;
-    if (strcmp(e, "split8") == 0) return (int)kSplit8;
-    if (strcmp(e, "wide") == 0) return (int)kWide;
-    if (strcmp(e, "wide_tail") == 0) return (int)kWideTail;
-    return -1;
-  }();
-  return v;
+  const char* e = getenv("SIDON_FLEXREL_VARIANT");
+  if (e == nullptr) return -1;
+  if (strcmp(e, "split8") == 0) return (int)kSplit8;
+  if (strcmp(e, "wide") == 0) return (int)kWide;
+  if (strcmp(e, "wide_tail") == 0) return (int)kWideTail;
+  if (strcmp(e, "w64") == 0) return (int)kW64;
+  return -1;
 }
 
-// Automatic choice, from launch timings on MI355X (H = 16, L = 500 .. 4800):
-// the 128-row kernel wins once its blocks fill more than about half of the
-// chip's compute units (its per-workgroup prologue and merge cost more than
-// the 64-row kernel's, its steps less); past one full round, the rows of the
-// part-full last round go to the 64-row kernel.
+// Automatic choice, from launch timings on MI355X (B = 1, H = 16,
+// L = 150 .. 4800): the two-workgroups-per-CU kernel is the fastest or level
+// with the fastest at every length (its key-step loop keeps the matrix core
+// busy with two wavefronts per SIMD; the 8-split kernel's steps cost more,
+// the 128-row kernel's blocks are too few below a full round of the chip).
+// K and V rows of different strides take the 8-split kernel.
 Variant choose_variant(int B, int H, int L, bool same_stride) {
-  if (!same_stride) return kSplit8;  // the wide kernel is built for K and V rows of one stride
+  (void)B;
+  (void)H;
+  (void)L;
+  if (!same_stride) return kSplit8;  // the other kernels are built for K and V rows of one stride
   const int f = forced_variant();
   if (f >= 0) return (Variant)f;
-  const long long blocks = (long long)B * H * ((L + wide_rows() - 1) / wide_rows());
-  const long long cus = sidon::compute_units();
-  if (blocks * 20 < cus * 11) return kSplit8;
-  if (blocks <= cus) return kWide;
-  return kWideTail;
+  return kW64;
 }
 
 // One launch: `rows` query rows per workgroup, nqb blocks per (b, h) from
 // query row row0.
 struct Launch {
-  Variant kernel;  // kSplit8 or kWide
+  Variant kernel;  // kSplit8, kWide or kW64
   int rows, splits, threads, nqb, row0;
   long long nwg;
 };
@@ -784,9 +784,9 @@ struct Plan {
 Launch launch_of(Variant kernel, int B, int H, int nqb, int row0) {
   Launch x;
   x.kernel = kernel;
-  x.rows = kernel == kWide ? wide_rows() : kRows;
-  x.splits = kernel == kWide ? 4 : kWaves;
-  x.threads = kernel == kWide ? wide_threads() : kThreads;
+  x.rows = kernel == kWide ? wide_rows() : kernel == kW64 ? w64_rows() : kRows;
+  x.splits = kernel == kSplit8 ? kWaves : 4;
+  x.threads = kernel == kWide ? wide_threads() : kernel == kW64 ? w64_threads() : kThreads;
   x.nqb = nqb;
   x.row0 = row0;
   x.nwg = (long long)B * H * nqb;
@@ -816,6 +816,8 @@ Plan plan_of(int B, int H, int L, bool same_stride = true) {
   }
   if (v == kWide) {
     pl.l[0] = launch_of(kWide, B, H, (L + wide_rows() - 1) / wide_rows(), 0);
+  } else if (v == kW64) {
+    pl.l[0] = launch_of(kW64, B, H, (L + w64_rows() - 1) / w64_rows(), 0);
   } else {
     pl.l[0] = launch_of(kSplit8, B, H, (L + kRows - 1) / kRows, 0);
   }
@@ -890,6 +892,8 @@ SIDON_API int sidon_flexrel_fwd(const void* q, const void* k, const void* v, con
     p.row0 = x.row0;
     if (x.kernel == kWide) {
       err = launch_wide(p, (int)x.nwg, true, s);
+    } else if (x.kernel == kW64) {
+      err = launch_w64(p, (int)x.nwg, true, s);
     } else {
       if (p.ksl == p.vsl)
         hipLaunchKernelGGL(flexrel_fwd_kernel<true>, dim3((unsigned)x.nwg), dim3(kThreads), 0, s, p);

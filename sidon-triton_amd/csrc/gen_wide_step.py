@@ -152,7 +152,7 @@ def branch(text):
 # wavefront per SIMD: VALU 5.44, v_exp_f32 9.14, MFMA 32x32x16 32.1 and
 # 16x16x32 16.6 on the matrix core) ----
 COSTS = {"valu": 5.44, "trans": 9.14, "permlane": 5.44, "mfma": 4.0, "salu": 4.0, "m0": 4.0, "dma": 4.0,
-         "lds": 4.0, "waitcnt": 4.0, "nop": 4.0, "branch": 4.0, "label": 0.0}
+         "lds": 4.0, "gload": 4.0, "waitcnt": 4.0, "nop": 4.0, "branch": 4.0, "label": 0.0}
 PIPE = {8: 32.0, 4: 16.0}
 
 
@@ -396,7 +396,7 @@ def required_states(p, c):
                 need = max(need, p.passes + 4)
         elif p.writes & touched:
             need = max(need, p.passes + 4)          # XDL write -> VALU/LDS/VMEM access
-        if c.kind in ("valu", "trans", "permlane", "lds") and p.srcc & c.writes:
+        if c.kind in ("valu", "trans", "permlane", "lds", "gload") and p.srcc & c.writes:
             need = max(need, 2 * p.passes)          # accumulator read late -> overwrite
     if p.kind in ("valu", "trans", "permlane") and c.kind == "mfma" and p.writes & (c.reads | c.srcc):
         need = max(need, 2)                         # VALU write -> MFMA read

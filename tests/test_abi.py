@@ -62,17 +62,24 @@ def test_launch_shape(sidon, B, H, L):
     assert s["key_splits"] >= 1
 
 
-def test_shape_choice(sidon):
-    """Without a device the library assumes 256 compute units: c3 (608
-    blocks of 128 rows) runs two whole rounds on the 128-row kernel and the
-    last 704 rows as 64-row blocks; c2 (192 blocks) the 128-row kernel; c1
-    (96 blocks, under half the chip) the 64-row kernel."""
+def test_shape_choice(sidon, monkeypatch):
+    """The automatic choice is the 64-row kernel with 4 key splits (two
+    workgroups per compute unit) at every length; SIDON_FLEXREL_VARIANT
+    forces another, read at every call.  Without a device the library
+    assumes 256 compute units: forced wide_tail runs c3 (608 blocks of 128
+    rows) as two whole rounds of 128-row blocks and the last 704 rows as
+    64-row blocks."""
+    monkeypatch.delenv("SIDON_FLEXREL_VARIANT", raising=False)
+    for L in (150, 750, 1500, 4800):
+        s = sidon._lib.launch_shape(1, 16, L)
+        assert s["queries_per_block"] == 64 and s["key_splits"] == 4 and s["threads_per_block"] == 256
+        assert s["workgroups"] == 16 * -(-L // 64)
+    monkeypatch.setenv("SIDON_FLEXREL_VARIANT", "wide_tail")
     c3 = sidon._lib.launch_shape(1, 16, 4800)
     assert c3["queries_per_block"] == 128 and c3["workgroups"] == 512 + 16 * 11
-    c2 = sidon._lib.launch_shape(1, 16, 1500)
-    assert c2["queries_per_block"] == 128 and c2["workgroups"] == 16 * 12
+    monkeypatch.setenv("SIDON_FLEXREL_VARIANT", "split8")
     c1 = sidon._lib.launch_shape(1, 16, 750)
-    assert c1["queries_per_block"] == 64 and c1["workgroups"] == 16 * 12
+    assert c1["queries_per_block"] == 64 and c1["key_splits"] == 8 and c1["threads_per_block"] == 512
 
 
 def _fwd(lib, **over):

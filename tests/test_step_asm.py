@@ -1,12 +1,16 @@
-"""The hand-scheduled key-step loop of flexrel_wide.hip (CPU only).
+"""The hand-scheduled key-step loops of flexrel_wide.hip and flexrel_w64.hip
+(CPU only).
 
-* The generator's checks (csrc/gen_wide_step.py) pass on the loop it writes,
-  and they catch planted mistakes: a removed wait state, a missing LDS wait.
-* Operand placement in the compiled kernel: the loop's text names fixed
-  registers (v0-v220, a0-a95, s64-s95); every register the compiler
-  substituted for a named operand must lie outside them.  (An operand bound
-  to a fixed register whose value is undefined at the loop entry lets the
-  compiler place other inputs inside it -- a mistake this test catches.)
+* The generators' checks (csrc/gen_wide_step.py, csrc/gen_w64_step.py) pass
+  on the loops they write, and they catch planted mistakes: a removed wait
+  state, a missing LDS wait.
+* Operand placement in the compiled kernels: a loop's text names fixed
+  registers (wide: v0-v220, a0-a95, s64-s95; 64-row: v0-v148, v152-v231,
+  s64-s95);
+  every register the compiler substituted for a named operand must lie
+  outside them.  (An operand bound to a fixed register whose value is
+  undefined at the loop entry lets the compiler place other inputs inside
+  it -- a mistake this test catches.)
 """
 
 from __future__ import annotations
@@ -24,10 +28,14 @@ REPO = Path(__file__).resolve().parents[1]
 CSRC = REPO / "sidon-triton_amd" / "csrc"
 
 
-def _gen():
-    spec = importlib.util.spec_from_file_location("gen_wide_step", CSRC / "gen_wide_step.py")
-    mod = importlib.util.module_from_spec(spec)
-    spec.loader.exec_module(mod)
+def _gen(name="gen_wide_step"):
+    sys.path.insert(0, str(CSRC))
+    try:
+        spec = importlib.util.spec_from_file_location(name, CSRC / f"{name}.py")
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+    finally:
+        sys.path.pop(0)
     return mod
 
 
@@ -67,7 +75,29 @@ def test_wait_check_catches_a_missing_lds_wait():
         gen.check_waits(planted + step, [("K", first), ("V", first), ("K", 1), ("V", 1)])
 
 
-def _compiled_loop():
+def test_w64_generator_checks_pass():
+    gen = _gen("gen_w64_step")
+    loop, step, cycles = gen.build()
+    assert len(step) > 100 and 500 < cycles < 1000
+    kinds = [i.kind for i in step]
+    # two blocks per step: 16 score, 16 PV and 4 row-sum products, 32 exp2
+    assert kinds.count("mfma") == 20 and kinds.count("trans") == 32
+    assert "a[" not in " ".join(i.text for i in loop)   # VGPRs only (two wavefronts per SIMD)
+
+
+def test_w64_wait_check_catches_a_missing_copy_wait():
+    gen = _gen("gen_w64_step")
+    _, step, _ = gen.build()
+    # plant: drop the vmcnt wait before the K operand reads of the K slot
+    waits = [k for k, ins in enumerate(step) if ins.text == "s_waitcnt vmcnt(4)"]
+    assert waits
+    planted = step[:waits[0]] + step[waits[0] + 1:]
+    with pytest.raises(AssertionError):
+        gen.check_waits(planted + planted, [])
+    gen.check_waits(step + step, [])
+
+
+def _compiled_loop(src="flexrel_wide.hip"):
     hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not Path(hipcc).exists():
         pytest.skip("hipcc not available")
@@ -79,7 +109,7 @@ def _compiled_loop():
     sidon_build.generate()
     flags = [f for f in sidon_build.HIP_FLAGS if f not in ("-fPIC", "-shared")]
     out = subprocess.run([hipcc, *flags, "--cuda-device-only", "-S", "-o", "-", f"-I{REPO / 'include'}",
-                          str(CSRC / "flexrel_wide.hip")], capture_output=True, text=True, timeout=600)
+                          str(CSRC / src)], capture_output=True, text=True, timeout=600)
     assert out.returncode == 0, out.stderr[-2000:]
     asm = out.stdout
     blocks = re.findall(r";;#ASMSTART\n(.*?);;#ASMEND", asm, re.S)
@@ -88,9 +118,9 @@ def _compiled_loop():
     return [ln.strip() for ln in loop[0].splitlines() if ln.strip()]
 
 
-def _template():
-    text = (CSRC / "flexrel_wide_step.inc").read_text()
-    body = text.split("#define SIDON_WIDE_LOOP \\\n", 1)[1]
+def _template(inc="flexrel_wide_step.inc", macro="SIDON_WIDE_LOOP"):
+    text = (CSRC / inc).read_text()
+    body = text.split(f"#define {macro} \\\n", 1)[1]
     return [m.group(1).strip() for m in re.finditer(r'"(.*?)\\n\\t"', body)]
 
 
@@ -102,9 +132,21 @@ def _reg_set(tok):
     return {(m.group(1), r) for r in range(lo, hi + 1)}
 
 
-def test_compiled_operands_avoid_the_loop_registers():
-    compiled = _compiled_loop()
-    template = [ln for ln in _template()]
+KERNELS = {
+    "wide": ("flexrel_wide.hip", "flexrel_wide_step.inc", "SIDON_WIDE_LOOP",
+             {("v", r) for r in range(0, 221)} | {("a", r) for r in range(0, 96)},
+             ("qbase", "laned", "g8", "ka0", "tv00", "ko0", "kl0", "m0", "nslow", "w", "q0", "lk")),
+    "w64": ("flexrel_w64.hip", "flexrel_w64_step.inc", "SIDON_W64_LOOP",
+            {("v", r) for r in list(range(0, 149)) + list(range(152, 232))},
+            ("qbase", "laned", "g8", "ka0", "ka3", "tv00", "ko0", "kl0", "m0", "m1", "nslow", "w", "q0", "lk")),
+}
+
+
+@pytest.mark.parametrize("kernel", sorted(KERNELS))
+def test_compiled_operands_avoid_the_loop_registers(kernel):
+    src, inc, macro, fixed, inputs = KERNELS[kernel]
+    compiled = _compiled_loop(src)
+    template = [ln for ln in _template(inc, macro)]
     assert len(compiled) == len(template)
     bound = {}
     for tpl, got in zip(template, compiled):
@@ -118,8 +160,7 @@ def test_compiled_operands_avoid_the_loop_registers():
             if a.startswith("%["):
                 name = a[2:a.index("]")]
                 bound.setdefault(name, set()).add(b)
-    reserved = ({("v", r) for r in range(0, 221)} | {("a", r) for r in range(0, 96)}
-                | {("s", r) for r in range(64, 96)})
+    reserved = fixed | {("s", r) for r in range(64, 96)}
     seen = {}
     for name, regs in bound.items():
         assert len(regs) == 1, (name, regs)   # one register per operand throughout the loop
@@ -130,5 +171,5 @@ def test_compiled_operands_avoid_the_loop_registers():
             assert not (rs & ors), (name, reg, other)
         seen[name] = rs
     # every input the loop reads is bound
-    for name in ("qbase", "laned", "g8", "ka0", "tv00", "ko0", "kl0", "m0", "nslow", "w", "q0", "lk"):
+    for name in inputs:
         assert name in bound, name
