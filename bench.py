@@ -25,8 +25,11 @@ import argparse
 import json
 import math
 import os
+import shutil
 import statistics
+import subprocess
 import sys
+import tempfile
 import time
 from pathlib import Path
 
@@ -36,8 +39,11 @@ sys.path.insert(0, str(ROOT))
 METRIC = "ms per 96 s chunk (8-layer attn, L=4800); TFLOP/s and % fp16 MFMA peak"
 PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
 B, H, L, D, LAYERS = 1, 16, 4800, 64, 8
-TRAFFIC_FILE = ROOT / "profiles" / "flexrel_fwd_c3_traffic.md"
 COPY_PROBE_BYTES = 256 << 20  # --copy-probe: one device copy of this many bytes
+XCDS = 8  # MI355X: GRBM_GUI_ACTIVE is summed over the 8 accelerator complex dies
+# Algorithmic HBM bytes of one c3 launch: q, k and v read once, the output
+# written once, the 73x64 table and the valid length.
+ALGO_BYTES = 3 * B * L * H * D * 2 + B * L * H * D * 2 + 73 * D * 2 + 4 * B
 
 
 def log(*a):
@@ -440,43 +446,61 @@ def encoder_flops(length, batch=1, heads=H, layers=LAYERS, inter=ENC_INTER, kern
     return gemm + conv + layers * attention_flops(batch * heads, length, length)
 
 
+ENC_LENGTHS = (750, 1500, 3000, 4800)               # 15, 30, 60, 96 s at 50 Hz
+ENC_H100_BY_L = {750: 1.3, 1500: 2.2, 3000: 4.4, 4800: ENC_H100_MS}  # reference README.md:37-40
+
+
 def run_encoder(torch, sidon, args) -> dict:
-    """The whole 8-layer conformer encoder on one 96 s chunk (features
-    [1, 4800, 160] -> hidden [1, 4800, 1024]), one HIP graph.  Parity is
-    tests/test_encoder_gpu.py."""
+    """The whole 8-layer conformer encoder (features [1, L, 160] -> hidden
+    [1, L, 1024]), one HIP graph per length, at the reference's published
+    chunk lengths 15/30/60/96 s (L = 750/1500/3000/4800).  The headline value
+    is the 96 s chunk.  Parity is tests/test_encoder_gpu.py."""
     dev = torch.device("cuda:0")
     packed = sidon.encoder.pack_weights(encoder_model_weights(torch))
     enc = sidon.encoder.HipEncoder(packed, dev)
-    gen = torch.Generator().manual_seed(8)
-    feats = torch.randn(B, L, ENC_FEATURES, generator=gen).to(dev)
-    lens = torch.full((B,), L, dtype=torch.int32, device=dev)
-    out = torch.empty(B, L, enc.hidden, device=dev)
-    ws = enc.workspace(B * L)
-    graph = sidon.graphs.BucketGraphs().capture(("encoder", L), lambda: enc(feats, lens, out=out, workspace=ws))
+    graphs = sidon.graphs.BucketGraphs()
     stream = torch.cuda.current_stream()
-    for _ in range(args.warmup):
-        graph.replay()
-    torch.cuda.synchronize()
     steps = max(1, args.steps)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(steps):
-        graph.replay()
-    e1.record(stream)
-    e1.synchronize()
-    ms = e0.elapsed_time(e1) / steps
+    rows, keep = [], []
+    lengths = [int(x) for x in args.enc_lengths.split(",")]
+    for length in lengths:
+        if length not in ENC_H100_BY_L:
+            raise SystemExit(f"--enc-lengths: {length} is not one of {sorted(ENC_H100_BY_L)}")
+        gen = torch.Generator().manual_seed(8)
+        feats = torch.randn(B, length, ENC_FEATURES, generator=gen).to(dev)
+        lens = torch.full((B,), length, dtype=torch.int32, device=dev)
+        out = torch.empty(B, length, enc.hidden, device=dev)
+        ws = enc.workspace(B * length)
+        keep.append((feats, lens, out, ws))
+        graph = graphs.capture(("encoder", length),
+                               lambda f=feats, n=lens, o=out, w=ws: enc(f, n, out=o, workspace=w))
+        for _ in range(args.warmup):
+            graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            graph.replay()
+        e1.record(stream)
+        e1.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        rows.append({"seconds": length // 50, "L": length, "ms": ms, "tflops": encoder_flops(length) / (ms * 1e-3) / 1e12,
+                     "h100_ms": ENC_H100_BY_L[length], "speedup_vs_h100": ENC_H100_BY_L[length] / ms})
+        log(f"encoder L={length}: {ms:.3f} ms")
+    ms = rows[-1]["ms"]
     return {
-        "metric": "ms per 96 s chunk (8-layer conformer encoder, L=4800)",
+        "metric": f"ms per {rows[-1]['seconds']} s chunk (8-layer conformer encoder, L={rows[-1]['L']})",
         "value": ms, "unit": "ms", "n_gpus": 1, "steps": steps, "warmup": args.warmup,
-        "higher_is_better": False, "scaling": "weak", "vs_baseline": ENC_H100_MS / ms,
-        "vs_baseline_note": "speed-up over the reference's published encoder stage, 7.6 ms per 96 s chunk on "
-                            "H100 SXM (README.md:40)",
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": rows[-1]["speedup_vs_h100"],
+        "vs_baseline_note": "speed-up over the reference's published encoder stage on H100 SXM at the last "
+                            "length: 1.3/2.2/4.4/7.6 ms for 15/30/60/96 s (README.md:37-40); per_length holds all",
         "dtype": "fp16",
         "data": "synthetic (features ~N(0,1); random-init weights of the architecture, see encoder_model_weights)",
         "config": {"workload": "encoder: feature projection + 8 conformer layers (FFN, attention, conv, FFN)",
                    "batch": B, "seq_len": L, "hidden": enc.hidden, "heads": H, "ffn": ENC_INTER,
-                   "conv_kernel": ENC_KERNEL, "layers": LAYERS},
-        "tflops": encoder_flops(L) / (ms * 1e-3) / 1e12,
+                   "conv_kernel": ENC_KERNEL, "layers": LAYERS, "lengths": lengths},
+        "tflops": rows[-1]["tflops"],
+        "per_length": rows,
     }
 
 
@@ -524,6 +548,127 @@ def run_frontend(torch, sidon, args) -> dict:
     }
 
 
+def under_profiler() -> bool:
+    """True inside a rocprofv3 run (the tool exports ROCPROF_* settings to
+    the program it runs)."""
+    return any(k.startswith("ROCPROF_") for k in os.environ)
+
+
+def _csv_rows(root: Path, suffix: str) -> list:
+    import csv
+    rows = []
+    for f in sorted(root.rglob(f"*{suffix}")):
+        with open(f, newline="") as fh:
+            rows.extend(csv.DictReader(fh))
+    return rows
+
+
+def _pmc_pass(prof: str, counters: list, probe: str, out: Path) -> tuple:
+    """One rocprofv3 counter pass (with its kernel trace) over a child
+    `bench.py <probe>`: per-dispatch counter sums {dispatch: {counter: value}}
+    and kernel names / durations (ns) by dispatch."""
+    cmd = [prof, "--kernel-trace", "--pmc", *counters, "--output-format", "csv", "-d", str(out), "-o", "p", "--",
+           sys.executable, str(ROOT / "bench.py"), probe]
+    subprocess.run(cmd, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL, timeout=300, check=True)
+    vals, names, dur = {}, {}, {}
+    for r in _csv_rows(out, "counter_collection.csv"):
+        d = r["Dispatch_Id"]
+        names[d] = r["Kernel_Name"]
+        vals.setdefault(d, {}).setdefault(r["Counter_Name"], 0.0)
+        vals[d][r["Counter_Name"]] += float(r["Counter_Value"])
+    for r in _csv_rows(out, "kernel_trace.csv"):
+        dur[r["Dispatch_Id"]] = float(r["End_Timestamp"]) - float(r["Start_Timestamp"])
+        names.setdefault(r["Dispatch_Id"], r["Kernel_Name"])
+    return vals, names, dur
+
+
+def measure_counters() -> dict:
+    """HBM traffic and clock of the attention kernel on the c3 shape,
+    measured in this run: four rocprofv3 counter passes over child
+    processes (FETCH_SIZE with GRBM_GUI_ACTIVE, then WRITE_SIZE, on
+    `--kernel-probe`: three launches of layer 0; the same two on
+    `--copy-probe`: device copies of 256 MiB, whose counter readings per
+    byte calibrate the KiB the counters report).  Runs before this process
+    touches the GPU; the children are started as child processes, never
+    exec'd.  The clock is GRBM_GUI_ACTIVE (busy cycles summed over the 8
+    XCDs) / 8 / kernel duration."""
+    prof = shutil.which("rocprofv3") or ("/opt/rocm/bin/rocprofv3" if Path("/opt/rocm/bin/rocprofv3").exists() else None)
+    if prof is None:
+        return {"error": "rocprofv3 not found"}
+    res = {"command": "rocprofv3 --kernel-trace --pmc <counter(s)> -- python bench.py --kernel-probe | --copy-probe"}
+    with tempfile.TemporaryDirectory(prefix="sidon_pmc_") as tmp:
+        tmp = Path(tmp)
+        per = {}
+        for key, counters, probe in (("kernel_fetch", ["FETCH_SIZE", "GRBM_GUI_ACTIVE"], "--kernel-probe"),
+                                     ("kernel_write", ["WRITE_SIZE"], "--kernel-probe"),
+                                     ("copy_fetch", ["FETCH_SIZE"], "--copy-probe"),
+                                     ("copy_write", ["WRITE_SIZE"], "--copy-probe")):
+            log(f"counters: {key} ({' '.join(counters)}) ...")
+            per[key] = _pmc_pass(prof, counters, probe, tmp / key)
+
+    res.update(summarize_counters(per))
+    return res
+
+
+def summarize_counters(per: dict) -> dict:
+    """Traffic and clock from the four passes of measure_counters: per pass
+    (counter sums by dispatch, kernel names by dispatch, durations in ns by
+    dispatch).  Medians over the dispatches of the attention kernel (name
+    containing "flexrel") and of the copy kernel (name containing "opy");
+    bytes = KiB read by the counter x 1024 x (copy bytes / copy KiB)."""
+    med = statistics.median
+    res = {}
+
+    def pick(key, word):
+        vals, names, dur = per[key]
+        ds = [d for d in vals if word in names.get(d, "")]
+        if not ds:
+            raise RuntimeError(f"no '{word}' dispatch in the {key} pass")
+        return ds, vals, dur
+
+    ds, vals, dur = pick("kernel_fetch", "flexrel")
+    res["kernel"] = per["kernel_fetch"][1][ds[0]]
+    res["dispatches"] = len(ds)
+    fetch_kib = med(vals[d]["FETCH_SIZE"] for d in ds)
+    grbm = med(vals[d]["GRBM_GUI_ACTIVE"] for d in ds)
+    dur_ns = med(dur[d] for d in ds if d in dur) if any(d in dur for d in ds) else None
+    ds_w, vals_w, _ = pick("kernel_write", "flexrel")
+    write_kib = med(vals_w[d]["WRITE_SIZE"] for d in ds_w)
+    cds, cvals, _ = pick("copy_fetch", "opy")
+    copy_fetch_kib = med(cvals[d]["FETCH_SIZE"] for d in cds)
+    cds_w, cvals_w, _ = pick("copy_write", "opy")
+    copy_write_kib = med(cvals_w[d]["WRITE_SIZE"] for d in cds_w)
+    copy_kib = COPY_PROBE_BYTES / 1024.0
+    f_fetch, f_write = copy_kib / copy_fetch_kib, copy_kib / copy_write_kib
+    traffic = fetch_kib * 1024.0 * f_fetch + write_kib * 1024.0 * f_write
+    res.update({"fetch_kib": fetch_kib, "write_kib": write_kib, "copy_fetch_kib": copy_fetch_kib,
+                "copy_write_kib": copy_write_kib, "fetch_factor": f_fetch, "write_factor": f_write,
+                "traffic_bytes": traffic, "algorithmic_bytes": ALGO_BYTES,
+                "traffic_over_algorithmic": traffic / ALGO_BYTES, "grbm_gui_active": grbm,
+                "kernel_ns_under_counters": dur_ns,
+                "sclk_mhz": (grbm / XCDS / dur_ns * 1e3) if dur_ns else None})
+    return res
+
+
+def kernel_probe() -> int:
+    """Three launches of the c3 attention (layer 0 inputs) for the counter
+    passes of measure_counters."""
+    import torch
+    from __graft_entry__ import load_package
+
+    sidon = load_package()
+    dev = torch.device("cuda:0")
+    h0, rels, projs = build_inputs(torch)
+    lens = torch.full((B,), L, dtype=torch.int32, device=dev)
+    qkv = qkv_of(torch, h0.to(dev), projs[0].to(dev))
+    out = torch.empty(B * L, H * D, dtype=torch.float16, device=dev)
+    rel = rels[0].to(dev)
+    for _ in range(3):
+        sidon.encoder_attention.flexrel_attention(qkv, B, H, rel, lens, out=out)
+    torch.cuda.synchronize()
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -537,12 +682,34 @@ def main() -> int:
     ap.add_argument("--workload", choices=["c3", "c4", "c5", "encoder", "frontend"], default="c3")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run 3 plain device copies of 256 MiB (calibrates the HBM byte counters)")
+    ap.add_argument("--kernel-probe", action="store_true",
+                    help="only run 3 launches of the c3 attention (the counter passes' workload)")
+    ap.add_argument("--enc-lengths", default=",".join(str(x) for x in ENC_LENGTHS),
+                    help="--workload encoder: comma-separated chunk lengths (frames) to time, last = headline")
+    ap.add_argument("--no-counters", action="store_true",
+                    help="skip the rocprofv3 counter passes (HBM traffic and clock of the c3 kernel)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py runs on one GPU only: this build has no multi-GPU path "
               "(each 96 s chunk is independent, so the natural scale-out is one process per GPU over "
               "chunks, with no collectives)", file=sys.stderr)
         return 2
+
+    if args.kernel_probe:
+        return kernel_probe()
+    counters = None
+    if args.workload == "c3" and not args.copy_probe:
+        # before this process touches the GPU: the passes run in child processes
+        if args.no_counters:
+            counters = {"skipped": "--no-counters"}
+        elif under_profiler():
+            counters = {"skipped": "running under rocprofv3 (its own passes measure the counters)"}
+        else:
+            try:
+                counters = measure_counters()
+            except (subprocess.SubprocessError, OSError, RuntimeError, KeyError, ValueError, ZeroDivisionError) as e:
+                counters = {"error": f"{type(e).__name__}: {e}"}
+        log(f"counters: {counters}")
 
     import torch
 
@@ -638,11 +805,8 @@ def main() -> int:
 
     extra["gpu_per_call_us"] = gpu_per_call(torch, sidon, dev)
 
-    traffic = None
-    if TRAFFIC_FILE.exists():
-        import re
-        m = re.search(r"HBM bytes per launch:\s*([0-9.eE+]+)", TRAFFIC_FILE.read_text())
-        traffic = float(m.group(1)) if m else None
+    traffic = counters.get("traffic_bytes") if counters else None
+    extra["counters"] = counters
 
     result = {
         "metric": METRIC,

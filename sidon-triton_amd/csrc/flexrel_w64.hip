@@ -67,6 +67,61 @@ static_assert(2 * kLdsBytes <= 160 * 1024, "two workgroups per CU");
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
+// Per-lane offsets, formed from the lane id.  The kernel forms them twice:
+// for the prologue and the key-step loop, and again from a fresh lane id
+// after the loop (for the rerun and the merge), so that no lane-dependent
+// value has to survive the loop, which holds all 256 registers.
+struct LaneTab {
+  int n, g;                        // query column in a 32-block, lane half
+  uint32_t voff[4], voff_last[4];  // tile copy offsets from base - 3072: any step, the last step
+  uint32_t kofs, kofs_last;        // K operand row offsets for global loads: any step, the last step
+  int kperm;                       // key row held by the K operand lane
+  int tr_off[2][2];                // V^T transpose-read offsets [hf][db] for hh = 0
+};
+
+// Tile copy lane offsets: LDS chunk position 64 i + lane = row 8 i + lane / 8,
+// swizzled chunk lane % 8; the last step T - 1 re-reads row LK - 1 (last_row
+// of the tile) for its rows past LK (their scores are masked).  K operands:
+// lane (m, g) of the MFMA A operand holds key row perm(m), dims 16 s + 8 g +
+// [0, 8) for k-step s (bytes 32 s + 16 g of the row).  V^T operands via
+// transpose reads (ds_read_b64_tr_b16): group G of 16 lanes, source lane
+// (a, bq) reads V[key0 + a][d0 + 4 bq .. +4) with key0 = 16 hh + 8 (G / 2) +
+// 4 hf and d0 = 32 db + 16 (G % 2).
+__device__ __forceinline__ LaneTab lane_tab(int lane, int64_t kstride, int last_row) {
+  LaneTab t;
+  t.n = lane & 31;
+  t.g = lane >> 5;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = 8 * i + (lane >> 3);
+    const int rc = min(r, last_row);
+    const uint32_t c16 = 16u * ((lane & 7) ^ tile_swz(r)) + 3072u - 1024u * i;
+    t.voff[i] = (uint32_t)(r * kstride) + c16;
+    t.voff_last[i] = (uint32_t)(rc * kstride) + c16;
+  }
+  t.kperm = mfma_row_perm(t.n);
+  t.kofs = (uint32_t)(t.kperm * kstride) + 16u * t.g;
+  t.kofs_last = (uint32_t)(min(t.kperm, last_row) * kstride) + 16u * t.g;
+  const int tr_G = lane >> 4, tr_a = (lane >> 2) & 3, tr_b = lane & 3;
+#pragma unroll
+  for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+    for (int db = 0; db < 2; ++db) {
+      const int row = 8 * (tr_G >> 1) + 4 * hf + tr_a;
+      const int chunk = 4 * db + 2 * (tr_G & 1) + (tr_b >> 1);
+      t.tr_off[hf][db] = row * 128 + ((chunk ^ tile_swz(row)) << 4) + 8 * (tr_b & 1);
+    }
+  return t;
+}
+
+// The lane id from an opaque instruction pair: never merged with an earlier
+// computation of it, so it is formed again instead of kept live.
+__device__ __forceinline__ int fresh_lane_id() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
+
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 flexrel_w64_kernel(const Params p) {
   __shared__ __attribute__((aligned(16))) char smem[kLdsBytes];
@@ -82,13 +137,42 @@ flexrel_w64_kernel(const Params p) {
   const int b = bh / p.H;
   const int h = bh - b * p.H;
 
-  int LK = p.L;
-  if (p.lens != nullptr) LK = min(max(p.lens[b], 0), p.L);
-  LK = __builtin_amdgcn_readfirstlane(LK);
   const int q0 = p.row0 + qblk * kRows;
   const float scale = p.scale;
-
   const _Float16* qbase = p.q + b * p.qsb + h * p.qsh;
+  // The valid length: a scalar load (uniform address), awaited at its first
+  // use below -- a vector load would be awaited with every copy in flight.
+  int lk_raw = p.L;
+  if (p.lens != nullptr) lk_raw = p.lens[__builtin_amdgcn_readfirstlane(b)];
+
+  // ---- prologue, part 1: the Q rows and rel rows, which do not depend on
+  // the valid length, are staged in LDS before that length is read ----
+  const uint32_t q_lds = (uint32_t)(uintptr_t)SIDON_LDS_PTR(char, smem + kQStageOff);
+  const uint32_t rel_lds = (uint32_t)(uintptr_t)SIDON_LDS_PTR(char, smem + kRelOff);
+  auto stage_rows = [&](uint32_t lds, const char* src, int64_t stride, int row0, int rmax, int nk) SIDON_INLINE {
+    // rows row0 + [0, 8 nk) of src (clamped to rmax) into LDS at lds, swizzled
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (i >= nk) break;
+      const int r = 8 * i + (lane >> 3);
+      const uint32_t off = (uint32_t)((min(row0 + r, rmax) - row0) * stride) + 16u * ((lane & 7) ^ tile_swz(r));
+      dma_1k(lds + 1024u * i, src + row0 * stride, off);
+    }
+  };
+  if (w < 2) {
+    const int row0 = min(q0 + 32 * w, p.L - 1);
+    stage_rows(q_lds + 4096u * w, reinterpret_cast<const char*>(qbase), (int64_t)p.qsl * 2, row0,
+               p.L - 1, 4);
+  } else {
+    stage_rows(rel_lds + 4096u * (w - 2), reinterpret_cast<const char*>(p.rel), kD * 2, 32 * (w - 2),
+               kNumPos - 1, 4);
+  }
+  if (w == 1)
+    stage_rows((uint32_t)(uintptr_t)SIDON_LDS_PTR(char, smem + kRel2Off), reinterpret_cast<const char*>(p.rel),
+               kD * 2, 64, kNumPos - 1, 2);
+
+  const int LK = __builtin_amdgcn_readfirstlane(min(max(lk_raw, 0), p.L));
+
   const char* kbase = reinterpret_cast<const char*>(p.k + b * p.ksb + h * p.ksh);
   const char* vbase = reinterpret_cast<const char*>(p.v + b * p.vsb + h * p.vsh);
   const int64_t kstride = (int64_t)p.ksl * 2;  // bytes (V rows have the same stride)
@@ -131,26 +215,8 @@ flexrel_w64_kernel(const Params p) {
   char* ring = smem + w * kTile;  // V slot 0 of this wavefront
   const uint32_t ring_lds = (uint32_t)(uintptr_t)SIDON_LDS_PTR(char, ring);
 
-  // Tile copy lane offsets (LDS chunk position 64 i + lane = row 8 i +
-  // lane / 8, swizzled chunk lane % 8), from base - 3072; the last step T - 1
-  // re-reads row LK - 1 for its rows past LK (their scores are masked).
-  uint32_t voff[4], voff_last[4];
   const int last_row = LK - 1 - (T - 1) * kStep;  // in [0, 31]
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = 8 * i + (lane >> 3);
-    const int rc = min(r, last_row);
-    const uint32_t c16 = 16u * ((lane & 7) ^ tile_swz(r)) + 3072u - 1024u * i;
-    voff[i] = (uint32_t)(r * kstride) + c16;
-    voff_last[i] = (uint32_t)(rc * kstride) + c16;
-  }
-  // K operands: lane (m, g) of the MFMA A operand holds key row perm(m) of
-  // the step, dims 16 s + 8 g + [0, 8) for k-step s (bytes 32 s + 16 g of
-  // the row); from global memory directly (prologue, rerun) or from the
-  // swizzled K slot (the loop).
-  const int kperm = mfma_row_perm(n);
-  const uint32_t kofs = (uint32_t)(kperm * kstride) + 16u * g;
-  const uint32_t kofs_last = (uint32_t)(min(kperm, last_row) * kstride) + 16u * g;
+  const LaneTab lt = lane_tab(lane, kstride, last_row);
   const bool ragged = LK % kStep != 0;  // step T - 1 straddles LK
 
   // Global step and tile base of processing index j (clamped to the last
@@ -158,57 +224,33 @@ flexrel_w64_kernel(const Params p) {
   auto step_of = [&](int j) SIDON_INLINE { return w + kWaves * u_of(min(j, nu - 1)); };
   // Copy of the K or V tile of processing index j into an LDS slot (K and V
   // rows share the stride, so one set of lane offsets serves both).
-  auto copy_v = [&](int j, uint32_t slot, const char* base) SIDON_INLINE {
-    const int t = step_of(j);
-    const char* gb = base + (int64_t)(t * kStep) * kstride - 3072;
-    const bool last = ragged && t == T - 1;
+  auto copy_v = [&](const LaneTab& t, int j, uint32_t slot, const char* base) SIDON_INLINE {
+    const int step = step_of(j);
+    const char* gb = base + (int64_t)(step * kStep) * kstride - 3072;
+    const bool last = ragged && step == T - 1;
     uint32_t o[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const uint32_t a = voff[i], c = voff_last[i];
+      const uint32_t a = t.voff[i], c = t.voff_last[i];
       o[i] = last ? c : a;
     }
     dma_tile(slot, gb, o[0], o[1], o[2], o[3]);
   };
-  auto load_k = [&](int j, h8 (&dst)[4]) SIDON_INLINE {
+  auto load_k = [&](const LaneTab& lt_, int j, h8 (&dst)[4]) SIDON_INLINE {
     const int t = step_of(j);
-    const char* gb = kbase + (int64_t)(t * kStep) * kstride + ((ragged && t == T - 1) ? kofs_last : kofs);
+    const char* gb = kbase + (int64_t)(t * kStep) * kstride + ((ragged && t == T - 1) ? lt_.kofs_last : lt_.kofs);
 #pragma unroll
     for (int s = 0; s < 4; ++s) dst[s] = *reinterpret_cast<const h8*>(gb + 32 * s);
   };
 
-  // ---- prologue: Q rows and rel rows staged in LDS, V(0) and K(2) copied
-  // into their slots, K(0) and K(1) loaded into registers -- all in flight
-  // at once ----
-  const uint32_t q_lds = (uint32_t)(uintptr_t)SIDON_LDS_PTR(char, smem + kQStageOff);
-  const uint32_t rel_lds = (uint32_t)(uintptr_t)SIDON_LDS_PTR(char, smem + kRelOff);
-  auto stage_rows = [&](uint32_t lds, const char* src, int64_t stride, int row0, int rmax, int nk) SIDON_INLINE {
-    // rows row0 + [0, 8 nk) of src (clamped to rmax) into LDS at lds, swizzled
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if (i >= nk) break;
-      const int r = 8 * i + (lane >> 3);
-      const uint32_t off = (uint32_t)((min(row0 + r, rmax) - row0) * stride) + 16u * ((lane & 7) ^ tile_swz(r));
-      dma_1k(lds + 1024u * i, src + row0 * stride, off);
-    }
-  };
-  if (w < 2) {
-    const int row0 = min(q0 + 32 * w, p.L - 1);
-    stage_rows(q_lds + 4096u * w, reinterpret_cast<const char*>(qbase), (int64_t)p.qsl * 2, row0,
-               p.L - 1, 4);
-  } else {
-    stage_rows(rel_lds + 4096u * (w - 2), reinterpret_cast<const char*>(p.rel), kD * 2, 32 * (w - 2),
-               kNumPos - 1, 4);
-  }
-  if (w == 1)
-    stage_rows((uint32_t)(uintptr_t)SIDON_LDS_PTR(char, smem + kRel2Off), reinterpret_cast<const char*>(p.rel),
-               kD * 2, 64, kNumPos - 1, 2);
+  // ---- prologue, part 2: V(0) and K(2) copied into their slots, K(0) and
+  // K(1) loaded into registers -- all in flight with the staging ----
   h8 kop[2][4];  // K operands, buffers 0 and 1
   if (active) {
-    copy_v(0, ring_lds, vbase);           // V(0) into V slot 0
-    copy_v(2, ring_lds + kKSlot, kbase);  // K(2) into the K slot
-    load_k(0, kop[0]);
-    load_k(1, kop[1]);
+    copy_v(lt, 0, ring_lds, vbase);           // V(0) into V slot 0
+    copy_v(lt, 2, ring_lds + kKSlot, kbase);  // K(2) into the K slot
+    load_k(lt, 0, kop[0]);
+    load_k(lt, 1, kop[1]);
     // the staged rows have landed: every memory operation but the 8 K
     // loads issued last (at least 8 younger ones follow the staging)
     wait_vmcnt<8>();
@@ -275,13 +317,6 @@ flexrel_w64_kernel(const Params p) {
   }
   lds_barrier();  // the q.rel table is complete
 
-  float qr_l[kBlocks], qr_r[kBlocks];
-#pragma unroll
-  for (int J = 0; J < kBlocks; ++J) {
-    qr_l[J] = qr_tab[(32 * J + n) * kQrStride];                // j - i <= -64
-    qr_r[J] = qr_tab[(32 * J + n) * kQrStride + kNumPos - 1];  // j - i >= 8
-  }
-
   f32x16 oacc[kBlocks][2];  // O^T: dims 32 db + 8 (i/4) + 4 g + i%4, query n
   float m_run[kBlocks];
   // Running row sums per block, accumulated on the matrix core (see rowsum
@@ -293,31 +328,16 @@ flexrel_w64_kernel(const Params p) {
   h8 pk[2][2] = {};      // fp16 probabilities [buffer][16-key half]
   h8 vop[2][2];          // V^T operands [hh][db] of one step
 
-  // V^T operands via transpose reads (ds_read_b64_tr_b16): group G of 16
-  // lanes, source lane (a, bq) reads V[key0 + a][d0 + 4 bq .. +4) with key0 =
-  // 16 hh + 8 (G / 2) + 4 hf and d0 = 32 db + 16 (G % 2).
-  const int tr_G = lane >> 4;
-  const int tr_a = (lane >> 2) & 3;
-  const int tr_b = lane & 3;
-  int tr_off[2][2];  // [hf][db] byte offset for hh = 0
-#pragma unroll
-  for (int hf = 0; hf < 2; ++hf)
-#pragma unroll
-    for (int db = 0; db < 2; ++db) {
-      const int row = 8 * (tr_G >> 1) + 4 * hf + tr_a;
-      const int chunk = 4 * db + 2 * (tr_G & 1) + (tr_b >> 1);
-      tr_off[hf][db] = row * 128 + ((chunk ^ tile_swz(row)) << 4) + 8 * (tr_b & 1);
-    }
-  auto load_v = [&](int sl) SIDON_INLINE {
+  auto load_v = [&](const LaneTab& t, int sl) SIDON_INLINE {
     const char* vt = ring + (sl ? kVSlot1 : 0);
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
 #pragma unroll
       for (int db = 0; db < 2; ++db) {
         const h4 lo = __builtin_bit_cast(
-            h4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(SIDON_LDS_PTR(s4, vt + tr_off[0][db] + 2048 * hh)));
+            h4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(SIDON_LDS_PTR(s4, vt + t.tr_off[0][db] + 2048 * hh)));
         const h4 hi = __builtin_bit_cast(
-            h4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(SIDON_LDS_PTR(s4, vt + tr_off[1][db] + 2048 * hh)));
+            h4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(SIDON_LDS_PTR(s4, vt + t.tr_off[1][db] + 2048 * hh)));
         vop[hh][db] = cat(lo, hi);
       }
     }
@@ -372,7 +392,9 @@ flexrel_w64_kernel(const Params p) {
   // per query from its own sum, never per wavefront, so one row cannot
   // change the rounding of another.  A query that needs no update keeps its
   // max, and its probabilities are the ones the hand-scheduled loop forms.
-  auto item = [&](int j, int u, int J) SIDON_INLINE {
+  auto item = [&](const LaneTab& t, const float (&ql)[kBlocks], const float (&qrr)[kBlocks], int j, int u,
+                  int J) SIDON_INLINE {
+    const int n = t.n, g = t.g;
     int k0 = (w + kWaves * u) * kStep;
     asm volatile("" : "+s"(k0));
     const int qlo = q0 + 32 * J;
@@ -381,7 +403,7 @@ flexrel_w64_kernel(const Params p) {
     const bool masked = k0 + kStep > LK;
     const bool band = !left && !right;
     const bool first = j == 0;
-    const float off = left ? qr_l[J] : (right ? qr_r[J] : 0.f);
+    const float off = left ? ql[J] : (right ? qrr[J] : 0.f);
     float y[16];
     if (band) {
       const float* qrow = qr_tab + (32 * J + n) * kQrStride;
@@ -455,6 +477,14 @@ flexrel_w64_kernel(const Params p) {
     // its steps again through `item` above, one step at a time.
     for (bool safe = false;; safe = true) {
       if (safe) {
+        // every lane-dependent value formed again (none survives the loop)
+        const LaneTab t1 = lane_tab(fresh_lane_id(), kstride, last_row);
+        float ql[kBlocks], qrr[kBlocks];
+#pragma unroll
+        for (int J = 0; J < kBlocks; ++J) {
+          ql[J] = qr_tab[(32 * J + t1.n) * kQrStride];
+          qrr[J] = qr_tab[(32 * J + t1.n) * kQrStride + kNumPos - 1];
+        }
 #pragma unroll
         for (int J = 0; J < kBlocks; ++J) {
           oacc[J][0] = f32x16{};
@@ -464,11 +494,11 @@ flexrel_w64_kernel(const Params p) {
         }
         for (int j = 0; j < nu; ++j) {
           const int u = u_of(j);
-          load_k(j, kop[0]);
+          load_k(t1, j, kop[0]);
           wait_lgkm0();  // the reads of the previous V tile are done
-          copy_v(j, ring_lds, vbase);
+          copy_v(t1, j, ring_lds, vbase);
           wait_vmcnt<0>();
-          load_v(0);
+          load_v(t1, 0);
 #pragma unroll
           for (int J = 0; J < kBlocks; ++J) {
             sacc[0] = qk(J, kop[0]);
@@ -476,7 +506,7 @@ flexrel_w64_kernel(const Params p) {
             // loop's plain form, and a query past the fp16 range must not
             // reach the row-sum product, where its inf would turn the sum of
             // the other query of its lane group into NaN)
-            item(j, u, J);
+            item(t1, ql, qrr, j, u, J);
             accumulate(J, 0);
             pv(J, 0);
           }
@@ -489,7 +519,7 @@ flexrel_w64_kernel(const Params p) {
       // the items before the first), probabilities and sums 0; no copy in
       // flight.
       wait_vmcnt<0>();
-      load_v(0);
+      load_v(lt, 0);
       sacc[0] = qk(0, kop[0]);
       // Loop state: j, the load bases (V of step j + 1, K of step j + 2) and
       // their advances for the plain steps (by 4 key steps, or across the
@@ -508,11 +538,11 @@ flexrel_w64_kernel(const Params p) {
       uint32_t ka[4], tv[2][2];
 #pragma unroll
       for (int s = 0; s < 4; ++s)
-        ka[s] = ring_lds + (uint32_t)(kperm * 128 + (((2 * s + g) ^ tile_swz(kperm)) << 4));
+        ka[s] = ring_lds + (uint32_t)(lt.kperm * 128 + (((2 * s + g) ^ tile_swz(lt.kperm)) << 4));
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
-        for (int db = 0; db < 2; ++db) tv[hf][db] = ring_lds + (uint32_t)tr_off[hf][db];
+        for (int db = 0; db < 2; ++db) tv[hf][db] = ring_lds + (uint32_t)lt.tr_off[hf][db];
       const uint32_t qbase_lds = (uint32_t)(uintptr_t)SIDON_LDS_PTR(float, qr_tab + n * kQrStride);
       const int laned = 8 * g - n;
       const int g8 = 8 * g;
@@ -534,9 +564,9 @@ flexrel_w64_kernel(const Params p) {
                      "{s[76:77]}"(djump), [nslow] "s"(nSlow), [w] "s"(w), [q0] "s"(q0), [lk] "s"(LK),
                      [tlast] "s"(tlast), [cl] "s"(cL), [nband] "s"(cR - cL), [ns] "s"(nS), [ue] "s"(uE),
                      [rowb] "s"(rowb), [kblo] "s"((uint32_t)kb), [kbhi] "s"((uint32_t)(kb >> 32)),
-                     [vblo] "s"((uint32_t)vb), [vbhi] "s"((uint32_t)(vb >> 32)), [ko0] "v"(voff[0]),
-                     [ko1] "v"(voff[1]), [ko2] "v"(voff[2]), [ko3] "v"(voff[3]), [kl0] "v"(voff_last[0]),
-                     [kl1] "v"(voff_last[1]), [kl2] "v"(voff_last[2]), [kl3] "v"(voff_last[3]),
+                     [vblo] "s"((uint32_t)vb), [vbhi] "s"((uint32_t)(vb >> 32)), [ko0] "v"(lt.voff[0]),
+                     [ko1] "v"(lt.voff[1]), [ko2] "v"(lt.voff[2]), [ko3] "v"(lt.voff[3]), [kl0] "v"(lt.voff_last[0]),
+                     [kl1] "v"(lt.voff_last[1]), [kl2] "v"(lt.voff_last[2]), [kl3] "v"(lt.voff_last[3]),
                      [ka0] "v"(ka[0]), [ka1] "v"(ka[1]), [ka2] "v"(ka[2]), [ka3] "v"(ka[3]), [tv00] "v"(tv[0][0]), [tv01] "v"(tv[0][1]),
                      [tv10] "v"(tv[1][0]), [tv11] "v"(tv[1][1]), [qbase] "v"(qbase_lds), [laned] "v"(laned),
                      [g8] "v"(g8)
@@ -558,30 +588,32 @@ flexrel_w64_kernel(const Params p) {
 
   // ---- merge the key splits ----
   lds_barrier();  // every wavefront is done with its ring and the q.rel table
+  const int lane1 = fresh_lane_id();
+  const int n1 = lane1 & 31, g1 = lane1 >> 5;
   float* mo = reinterpret_cast<float*>(smem);
   float* ml = reinterpret_cast<float*>(smem + kMergeMlOff);
 #pragma unroll
   for (int J = 0; J < kBlocks; ++J) {
-    float* dst = mo + (w * kRows + 32 * J + n) * kMergeStride;
+    float* dst = mo + (w * kRows + 32 * J + n1) * kMergeStride;
 #pragma unroll
     for (int db = 0; db < 2; ++db) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const f4 val = {oacc[J][db][4 * j], oacc[J][db][4 * j + 1], oacc[J][db][4 * j + 2], oacc[J][db][4 * j + 3]};
-        *reinterpret_cast<f4*>(dst + 32 * db + 8 * j + 4 * g) = val;
+        *reinterpret_cast<f4*>(dst + 32 * db + 8 * j + 4 * g1) = val;
       }
     }
-    if (g == 0) {
-      ml[(w * kRows + 32 * J + n) * 2] = m_run[J];
-      ml[(w * kRows + 32 * J + n) * 2 + 1] = lsum[J][0];
+    if (g1 == 0) {
+      ml[(w * kRows + 32 * J + n1) * 2] = m_run[J];
+      ml[(w * kRows + 32 * J + n1) * 2 + 1] = lsum[J][0];
     }
   }
   lds_barrier();
 
   // Wavefront w finalises rows 16 w + [0, 16), four lanes per row, 16 dims
   // per lane.
-  const int r = 16 * w + (lane >> 2);
-  const int c = 16 * (lane & 3);
+  const int r = 16 * w + (lane1 >> 2);
+  const int c = 16 * (lane1 & 3);
   float mmax = -INFINITY;
 #pragma unroll
   for (int s = 0; s < kWaves; ++s) mmax = fmaxf(mmax, ml[(s * kRows + r) * 2]);

@@ -55,3 +55,31 @@ def test_host_cpu_reports_this_host():
     assert info["cpu_count"] == os.cpu_count()
     assert 1 <= info["affinity"] <= os.cpu_count()
     assert info["model"] is None or isinstance(info["model"], str)
+
+
+def test_summarize_counters_known_answer():
+    """Traffic = KiB read by each counter x 1024 x (copy bytes / copy KiB),
+    medians over the attention dispatches only; clock = GRBM_GUI_ACTIVE / 8
+    XCDs / duration.  Fabricated readings with a closed-form answer: the copy
+    passes read half the copied KiB for FETCH_SIZE (factor 2) and all of it
+    for WRITE_SIZE (factor 1)."""
+    import bench
+
+    copy_kib = bench.COPY_PROBE_BYTES / 1024.0
+    names = {"1": "flexrel_w64_kernel", "2": "flexrel_w64_kernel", "3": "flexrel_w64_kernel", "9": "Cijk_gemm"}
+    fetch = {"1": {"FETCH_SIZE": 100.0, "GRBM_GUI_ACTIVE": 8 * 2000.0}, "2": {"FETCH_SIZE": 110.0, "GRBM_GUI_ACTIVE": 8 * 2100.0},
+             "3": {"FETCH_SIZE": 120.0, "GRBM_GUI_ACTIVE": 8 * 2200.0}, "9": {"FETCH_SIZE": 1e9, "GRBM_GUI_ACTIVE": 1.0}}
+    dur = {"1": 1000.0, "2": 1000.0, "3": 1000.0, "9": 5.0}
+    write = {"1": {"WRITE_SIZE": 40.0}, "2": {"WRITE_SIZE": 50.0}, "3": {"WRITE_SIZE": 60.0}, "9": {"WRITE_SIZE": 1e9}}
+    cnames = {"7": "__amd_rocclr_copyBuffer"}
+    per = {"kernel_fetch": (fetch, names, dur), "kernel_write": (write, names, {}),
+           "copy_fetch": ({"7": {"FETCH_SIZE": copy_kib / 2}}, cnames, {}),
+           "copy_write": ({"7": {"WRITE_SIZE": copy_kib}}, cnames, {})}
+    res = bench.summarize_counters(per)
+    assert res["dispatches"] == 3
+    assert math.isclose(res["fetch_factor"], 2.0) and math.isclose(res["write_factor"], 1.0)
+    assert math.isclose(res["traffic_bytes"], 110.0 * 1024 * 2 + 50.0 * 1024)
+    assert math.isclose(res["sclk_mhz"], 2100.0 / 1000.0 * 1e3)   # 2100 cycles per XCD in 1000 ns
+    assert math.isclose(res["traffic_over_algorithmic"], res["traffic_bytes"] / bench.ALGO_BYTES)
+    # the c3 algorithmic bytes: q, k, v read and the output written once, the table, the length
+    assert bench.ALGO_BYTES == 4 * 4800 * 1024 * 2 + 73 * 64 * 2 + 4
