@@ -251,9 +251,10 @@ flexrel_w64_kernel(const Params p) {
     copy_v(lt, 2, ring_lds + kKSlot, kbase);  // K(2) into the K slot
     load_k(lt, 0, kop[0]);
     load_k(lt, 1, kop[1]);
-    // the staged rows have landed: every memory operation but the 8 K
-    // loads issued last (at least 8 younger ones follow the staging)
-    wait_vmcnt<8>();
+    // the staged rows have landed: every memory operation but the 16 issued
+    // last (the two copies above, then the K loads: at least 8 instructions
+    // of 16 bytes per lane)
+    wait_vmcnt<16>();
   } else {
     wait_vmcnt<0>();
   }
@@ -315,7 +316,6 @@ flexrel_w64_kernel(const Params p) {
       }
     }
   }
-  lds_barrier();  // the q.rel table is complete
 
   f32x16 oacc[kBlocks][2];  // O^T: dims 32 db + 8 (i/4) + 4 g + i%4, query n
   float m_run[kBlocks];
@@ -469,6 +469,19 @@ flexrel_w64_kernel(const Params p) {
   }
 
   if (active) {
+    // Entry state of the loop: S^T of item (0, 0) in sacc[0], K(0) and K(1)
+    // in the two K buffers, K(2) in the K slot, V(0) in ring slot 0 and in
+    // the V operands (finite operands for the zero probabilities of the
+    // items before the first), probabilities and sums 0; no copy in flight.
+    // (Formed before the barrier below, behind which the slowest
+    // wavefront's part of the q.rel table lands.)
+    wait_vmcnt<0>();
+    load_v(lt, 0);
+    sacc[0] = qk(0, kop[0]);
+  }
+  lds_barrier();  // the q.rel table is complete
+
+  if (active) {
     // The first pass runs every step through the hand-scheduled loop of
     // flexrel_w64_step.inc; it checks no step sum: a probability past the
     // fp16 range becomes inf and makes its block's running sum non-finite
@@ -513,14 +526,6 @@ flexrel_w64_kernel(const Params p) {
         }
         break;
       }
-      // Entry state of the loop: S^T of item (0, 0) in sacc[0], K(0) and
-      // K(1) in the two K buffers, K(2) in the K slot, V(0) in ring slot 0
-      // and in the V operands (finite operands for the zero probabilities of
-      // the items before the first), probabilities and sums 0; no copy in
-      // flight.
-      wait_vmcnt<0>();
-      load_v(lt, 0);
-      sacc[0] = qk(0, kop[0]);
       // Loop state: j, the load bases (V of step j + 1, K of step j + 2) and
       // their advances for the plain steps (by 4 key steps, or across the
       // band at index jump), the scalars of the processing order, and the

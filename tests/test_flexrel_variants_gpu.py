@@ -1,0 +1,103 @@
+"""GPU parity of every attention kernel variant, not only the automatic
+choice (needs an MI355X).
+
+`SIDON_FLEXREL_VARIANT` (read by the library at every call) forces the
+8-split kernel of flexrel_fwd.hip, the 128-row kernel of flexrel_wide.hip
+(alone, and as whole rounds plus an 8-split tail), or the 64-row kernel of
+flexrel_w64.hip; K and V rows of different strides take the 8-split kernel
+without being forced.  Each is checked against the float64 oracle at the
+north-star bar on ragged and padded shapes, for the same results contract:
+keys past the valid length (refilled with finite garbage, which sends the
+loop's overflow check into its rerun) leave the valid rows bit-identical.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import seeded_inputs
+from oracle.flexrel_oracle import flexrel_reference
+from test_flexrel_gpu import DEV, assert_parity, run
+
+pytestmark = pytest.mark.gpu
+
+VARIANTS = ["split8", "wide", "wide_tail", "w64"]
+SHAPES = [
+    # (B, H, L, lens)
+    (1, 2, 33, [20]),
+    (1, 3, 127, [127]),
+    (2, 2, 200, [200, 173]),
+    (3, 2, 300, [300, 64, 129]),
+    (1, 4, 513, [513]),
+    (1, 16, 750, None),
+]
+
+
+@pytest.fixture
+def variant(request, monkeypatch):
+    monkeypatch.setenv("SIDON_FLEXREL_VARIANT", request.param)
+    return request.param
+
+
+@pytest.mark.parametrize("variant", VARIANTS, indirect=True)
+@pytest.mark.parametrize("B,H,L,lens", SHAPES)
+def test_variant_parity(sidon, variant, B, H, L, lens):
+    q, k, v, rel = seeded_inputs(B, H, L, seed=1000 + L)
+    got = run(sidon, q, k, v, rel, lens).float().cpu().numpy()
+    lk = lens if lens is not None else [L] * B
+    ref = np.zeros_like(got, dtype=np.float64)
+    for b in range(B):
+        if lk[b]:
+            ref[b:b + 1, :, :lk[b]] = flexrel_reference(q.numpy()[b:b + 1, :, :lk[b]], k.numpy()[b:b + 1, :, :lk[b]],
+                                                        v.numpy()[b:b + 1, :, :lk[b]], rel.numpy())
+    assert_parity(ref, got, lk, f"{variant} B={B} H={H} L={L}")
+
+
+@pytest.mark.parametrize("variant", VARIANTS, indirect=True)
+def test_variant_padding_garbage_bit_identical(sidon, variant):
+    """c2's bucket: L=1500, LK=1463; rows past LK refilled with +-60000."""
+    L, LK = 1500, 1463
+    q, k, v, rel = seeded_inputs(1, 16, L, seed=2)
+    k[:, :, LK:] = 0
+    v[:, :, LK:] = 0
+    got = run(sidon, q, k, v, rel, [LK])
+    ref = flexrel_reference(q.numpy()[:, :, :LK], k.numpy()[:, :, :LK], v.numpy()[:, :, :LK], rel.numpy())
+    assert_parity(ref, got.float().cpu().numpy()[:, :, :LK], [LK], f"{variant} c2")
+    gen = torch.Generator().manual_seed(22)
+    k2, v2, q2 = k.clone(), v.clone(), q.clone()
+    for t in (k2, v2, q2):
+        t[:, :, LK:] = ((torch.rand(t[:, :, LK:].shape, generator=gen) * 2 - 1) * 60000).half()
+    got2 = run(sidon, q2, k2, v2, rel, [LK])
+    assert torch.equal(got[:, :, :LK], got2[:, :, :LK]), f"{variant}: keys past LK changed valid rows"
+
+
+@pytest.mark.parametrize("variant", ["wide_tail", "w64"], indirect=True)
+def test_variant_c3_shape(sidon, variant):
+    """L=4800, H=16: the grids of several rounds (and the wide kernel's tail launch); 2 heads checked."""
+    q, k, v, rel = seeded_inputs(1, 16, 4800, seed=3)
+    got = run(sidon, q, k, v, rel).float().cpu().numpy()
+    assert np.isfinite(got).all()
+    heads = [0, 15]
+    ref = flexrel_reference(q.numpy()[:, heads], k.numpy()[:, heads], v.numpy()[:, heads], rel.numpy())
+    assert_parity(ref, got[:, heads], [4800], f"{variant} c3")
+
+
+def test_different_kv_strides_take_the_8_split_kernel(sidon, monkeypatch):
+    """K and V views of different row strides (V a slice of a wider buffer):
+    the automatic choice falls back to the 8-split kernel; same results
+    as contiguous copies of the same values."""
+    monkeypatch.delenv("SIDON_FLEXREL_VARIANT", raising=False)
+    B, H, L = 1, 4, 300
+    q, k, v, rel = seeded_inputs(B, H, L, seed=61)
+    wide = torch.zeros(B, H, L, 128, dtype=torch.float16)
+    wide[..., 32:96] = v
+    v_view = wide.to(DEV)[..., 32:96]          # row stride 128 elements, K's is 64
+    out = sidon.flexrel.flexrel_attention(q.to(DEV), k.to(DEV), v_view, rel.to(DEV))
+    torch.cuda.synchronize()
+    ref = flexrel_reference(q.numpy(), k.numpy(), v.numpy(), rel.numpy())
+    assert_parity(ref, out.float().cpu().numpy(), [L], "kv-strides")
+    monkeypatch.setenv("SIDON_FLEXREL_VARIANT", "split8")
+    out8 = run(sidon, q, k, v, rel)
+    assert torch.equal(out, out8)
