@@ -20,10 +20,11 @@
 // Per wavefront and step (32 keys), for each block J: S^T = K . Q^T (4
 // v_mfma_f32_32x32x16_f16, Q^T in registers), the exp2 softmax with the lazily
 // updated running max of flexrel_fwd.hip, the row sums on the matrix core (2
-// v_mfma_f32_16x16x32_f16) and O^T += V^T . P^T (4 MFMAs).  The K operands
-// come from global memory straight into registers (two buffers); only the V
-// tiles pass through LDS (a two-slot ring per wavefront, copied with
-// global_load_lds_dwordx4 and read transposed with ds_read_b64_tr_b16).
+// v_mfma_f32_16x16x32_f16) and O^T += V^T . P^T (4 MFMAs).  K and V tiles
+// pass through LDS, copied with global_load_lds_dwordx4: K through one slot
+// per wavefront (tile j + 3 copied once tile j + 2 is in registers; two
+// register buffers), V through a two-slot ring read transposed with
+// ds_read_b64_tr_b16.
 // The key-step loop is hand-scheduled assembly (flexrel_w64_step.inc,
 // written and checked by gen_w64_step.py); a wavefront whose probabilities
 // leave the fp16 range reruns its steps through the C++ code below, which

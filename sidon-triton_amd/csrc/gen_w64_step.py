@@ -9,11 +9,12 @@ flexrel_w64.hip computes for it, so the C++ rerun reproduces every query
 that did not overflow bit for bit.  Differences from the 128-row loop:
 
 * two phases per key step (blocks 0 and 1);
-* the K operands of a step come straight from global memory into VGPRs
-  (two buffers; K(j + 2) is loaded in phase 0 of step j, after the score
-  product of item (j, 1) read K(j)), so LDS holds only the V ring
-  (two slots per wavefront; V(j + 1) is copied in phase 0 of step j) and two
-  workgroups fit on a compute unit;
+* K tiles pass through one LDS slot per wavefront into two register
+  buffers: in phase 0 of step j, after the score product of item (j, 1)
+  read K(j), K(j + 2) is read from the slot into that buffer, and then
+  K(j + 3) is copied into the slot; V tiles use a two-slot ring (V(j + 1) is
+  copied in phase 0 of step j, V(j) read transposed in phase 1), so three
+  4 KB tiles per wavefront and two workgroups fit on a compute unit;
 * registers (per wavefront, at most 256 with two wavefronts per SIMD; all
   of them VGPRs: a kernel that names AGPRs gets at most half of its 256 as
   VGPRs):
