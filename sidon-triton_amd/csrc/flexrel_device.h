@@ -1,7 +1,9 @@
 // flexrel_device.h -- device helpers and launch parameters shared by the
 // relative_key attention kernels (flexrel_fwd.hip: 64 query rows per
 // workgroup, 8 key splits; flexrel_wide.hip: 128 query rows per wavefront,
-// 4 key splits).  Internal to the library.
+// 4 key splits; flexrel_w64.hip: 64 rows per wavefront, 4 key splits, two
+// workgroups per compute unit; flexrel_w32.hip: 32 rows per wavefront, 4 key
+// splits, for short sequences).  Internal to the library.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -132,6 +134,59 @@ __device__ __forceinline__ int xcd_linear(int bid, int nwg) {
   return (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + (bid >> 3);
 }
 
+// Per-lane offsets of the 4-wavefront kernels (flexrel_w64.hip,
+// flexrel_w32.hip), formed from the lane id.
+struct LaneTab {
+  int n, g;                        // query column in a 32-block, lane half
+  uint32_t voff[4], voff_last[4];  // tile copy offsets from base - 3072: any step, the last step
+  uint32_t kofs, kofs_last;        // K operand row offsets for global loads: any step, the last step
+  int kperm;                       // key row held by the K operand lane
+  int tr_off[2][2];                // V^T transpose-read offsets [hf][db] for hh = 0
+};
+
+// Tile copy lane offsets: LDS chunk position 64 i + lane = row 8 i + lane / 8,
+// swizzled chunk lane % 8; the last step T - 1 re-reads row LK - 1 (last_row
+// of the tile) for its rows past LK (their scores are masked).  K operands:
+// lane (m, g) of the MFMA A operand holds key row perm(m), dims 16 s + 8 g +
+// [0, 8) for k-step s (bytes 32 s + 16 g of the row).  V^T operands via
+// transpose reads (ds_read_b64_tr_b16): group G of 16 lanes, source lane
+// (a, bq) reads V[key0 + a][d0 + 4 bq .. +4) with key0 = 16 hh + 8 (G / 2) +
+// 4 hf and d0 = 32 db + 16 (G % 2).
+__device__ __forceinline__ LaneTab lane_tab(int lane, int64_t kstride, int last_row) {
+  LaneTab t;
+  t.n = lane & 31;
+  t.g = lane >> 5;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = 8 * i + (lane >> 3);
+    const int rc = min(r, last_row);
+    const uint32_t c16 = 16u * ((lane & 7) ^ tile_swz(r)) + 3072u - 1024u * i;
+    t.voff[i] = (uint32_t)(r * kstride) + c16;
+    t.voff_last[i] = (uint32_t)(rc * kstride) + c16;
+  }
+  t.kperm = mfma_row_perm(t.n);
+  t.kofs = (uint32_t)(t.kperm * kstride) + 16u * t.g;
+  t.kofs_last = (uint32_t)(min(t.kperm, last_row) * kstride) + 16u * t.g;
+  const int tr_G = lane >> 4, tr_a = (lane >> 2) & 3, tr_b = lane & 3;
+#pragma unroll
+  for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+    for (int db = 0; db < 2; ++db) {
+      const int row = 8 * (tr_G >> 1) + 4 * hf + tr_a;
+      const int chunk = 4 * db + 2 * (tr_G & 1) + (tr_b >> 1);
+      t.tr_off[hf][db] = row * 128 + ((chunk ^ tile_swz(row)) << 4) + 8 * (tr_b & 1);
+    }
+  return t;
+}
+
+// The lane id from an opaque instruction pair: never merged with an earlier
+// computation of it, so it is formed again instead of kept live.
+__device__ __forceinline__ int fresh_lane_id() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
+
 }  // namespace sidon_flexrel
 
 // Launch of the 128-row kernel (flexrel_wide.hip) for workgroups
@@ -145,4 +200,9 @@ hipError_t launch_wide(const Params& p, int nwg, bool same_stride, hipStream_t s
 int w64_rows();
 int w64_threads();
 hipError_t launch_w64(const Params& p, int nwg, bool same_stride, hipStream_t stream);
+// Launch of the 32-row kernel (flexrel_w32.hip), with p.nqb = query blocks
+// of 32 rows per (b, h).
+int w32_rows();
+int w32_threads();
+hipError_t launch_w32(const Params& p, int nwg, bool same_stride, hipStream_t stream);
 }  // namespace sidon_flexrel

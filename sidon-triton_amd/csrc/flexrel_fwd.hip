@@ -738,10 +738,11 @@ namespace {
 // (flexrel_w64.hip); the 128-row wavefront with 4 key splits (flexrel_wide.hip)
 // over all rows; and the wide kernel over as many 128-row blocks as fill
 // whole rounds of the chip, the remaining rows then running on the 8-split
-// kernel in a second launch.
-enum Variant { kSplit8 = 0, kWide = 1, kWideTail = 2, kW64 = 3 };
+// kernel in a second launch; the 32-row workgroup with 4 key splits
+// (flexrel_w32.hip) for short sequences.
+enum Variant { kSplit8 = 0, kWide = 1, kWideTail = 2, kW64 = 3, kW32 = 4 };
 
-// SIDON_FLEXREL_VARIANT=split8|wide|wide_tail|w64 forces one variant (A/B
+// SIDON_FLEXREL_VARIANT=split8|wide|wide_tail|w64|w32 forces one variant (A/B
 // timing and tests; read at every call); unset or "auto" picks by shape.
 int forced_variant() {
   const char* e = getenv("SIDON_FLEXREL_VARIANT");
@@ -750,29 +751,33 @@ int forced_variant() {
   if (strcmp(e, "wide") == 0) return (int)kWide;
   if (strcmp(e, "wide_tail") == 0) return (int)kWideTail;
   if (strcmp(e, "w64") == 0) return (int)kW64;
+  if (strcmp(e, "w32") == 0) return (int)kW32;
   return -1;
 }
 
 // Automatic choice, from launch timings on MI355X (B = 1, H = 16,
-// L = 150 .. 4800): the two-workgroups-per-CU kernel is the fastest or level
-// with the fastest at every length (its key-step loop keeps the matrix core
-// busy with two wavefronts per SIMD; the 8-split kernel's steps cost more,
-// the 128-row kernel's blocks are too few below a full round of the chip).
-// K and V rows of different strides take the 8-split kernel.
+// L = 150 .. 4800): when the 32-row kernel's workgroups (B H ceil(L / 32))
+// fit one per compute unit, it is the fastest (its critical path -- q.rel
+// table, steps near the diagonal, merge -- is half the 64-row kernel's, and
+// no workgroup shares a compute unit); above that, the two-workgroups-per-CU
+// 64-row kernel is the fastest or level with the fastest at every length
+// (its key-step loop keeps the matrix core busy with two wavefronts per
+// SIMD; the 32-row kernel's pairs contend in their latency-bound phases, the
+// 8-split kernel's steps cost more, the 128-row kernel's blocks are too few
+// below a full round of the chip).  K and V rows of different strides take
+// the 8-split kernel.
 Variant choose_variant(int B, int H, int L, bool same_stride) {
-  (void)B;
-  (void)H;
-  (void)L;
   if (!same_stride) return kSplit8;  // the other kernels are built for K and V rows of one stride
   const int f = forced_variant();
   if (f >= 0) return (Variant)f;
-  return kW64;
+  const long long w32_blocks = (long long)B * H * ((L + w32_rows() - 1) / w32_rows());
+  return w32_blocks <= sidon::compute_units() ? kW32 : kW64;
 }
 
 // One launch: `rows` query rows per workgroup, nqb blocks per (b, h) from
 // query row row0.
 struct Launch {
-  Variant kernel;  // kSplit8, kWide or kW64
+  Variant kernel;  // kSplit8, kWide, kW64 or kW32
   int rows, splits, threads, nqb, row0;
   long long nwg;
 };
@@ -784,9 +789,12 @@ struct Plan {
 Launch launch_of(Variant kernel, int B, int H, int nqb, int row0) {
   Launch x;
   x.kernel = kernel;
-  x.rows = kernel == kWide ? wide_rows() : kernel == kW64 ? w64_rows() : kRows;
+  x.rows = kernel == kWide ? wide_rows() : kernel == kW64 ? w64_rows() : kernel == kW32 ? w32_rows() : kRows;
   x.splits = kernel == kSplit8 ? kWaves : 4;
-  x.threads = kernel == kWide ? wide_threads() : kernel == kW64 ? w64_threads() : kThreads;
+  x.threads = kernel == kWide  ? wide_threads()
+              : kernel == kW64 ? w64_threads()
+              : kernel == kW32 ? w32_threads()
+                               : kThreads;
   x.nqb = nqb;
   x.row0 = row0;
   x.nwg = (long long)B * H * nqb;
@@ -818,6 +826,8 @@ Plan plan_of(int B, int H, int L, bool same_stride = true) {
     pl.l[0] = launch_of(kWide, B, H, (L + wide_rows() - 1) / wide_rows(), 0);
   } else if (v == kW64) {
     pl.l[0] = launch_of(kW64, B, H, (L + w64_rows() - 1) / w64_rows(), 0);
+  } else if (v == kW32) {
+    pl.l[0] = launch_of(kW32, B, H, (L + w32_rows() - 1) / w32_rows(), 0);
   } else {
     pl.l[0] = launch_of(kSplit8, B, H, (L + kRows - 1) / kRows, 0);
   }
@@ -894,6 +904,8 @@ SIDON_API int sidon_flexrel_fwd(const void* q, const void* k, const void* v, con
       err = launch_wide(p, (int)x.nwg, true, s);
     } else if (x.kernel == kW64) {
       err = launch_w64(p, (int)x.nwg, true, s);
+    } else if (x.kernel == kW32) {
+      err = launch_w32(p, (int)x.nwg, true, s);
     } else {
       if (p.ksl == p.vsl)
         hipLaunchKernelGGL(flexrel_fwd_kernel<true>, dim3((unsigned)x.nwg), dim3(kThreads), 0, s, p);

@@ -68,60 +68,10 @@ static_assert(2 * kLdsBytes <= 160 * 1024, "two workgroups per CU");
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-// Per-lane offsets, formed from the lane id.  The kernel forms them twice:
-// for the prologue and the key-step loop, and again from a fresh lane id
-// after the loop (for the rerun and the merge), so that no lane-dependent
-// value has to survive the loop, which holds all 256 registers.
-struct LaneTab {
-  int n, g;                        // query column in a 32-block, lane half
-  uint32_t voff[4], voff_last[4];  // tile copy offsets from base - 3072: any step, the last step
-  uint32_t kofs, kofs_last;        // K operand row offsets for global loads: any step, the last step
-  int kperm;                       // key row held by the K operand lane
-  int tr_off[2][2];                // V^T transpose-read offsets [hf][db] for hh = 0
-};
-
-// Tile copy lane offsets: LDS chunk position 64 i + lane = row 8 i + lane / 8,
-// swizzled chunk lane % 8; the last step T - 1 re-reads row LK - 1 (last_row
-// of the tile) for its rows past LK (their scores are masked).  K operands:
-// lane (m, g) of the MFMA A operand holds key row perm(m), dims 16 s + 8 g +
-// [0, 8) for k-step s (bytes 32 s + 16 g of the row).  V^T operands via
-// transpose reads (ds_read_b64_tr_b16): group G of 16 lanes, source lane
-// (a, bq) reads V[key0 + a][d0 + 4 bq .. +4) with key0 = 16 hh + 8 (G / 2) +
-// 4 hf and d0 = 32 db + 16 (G % 2).
-__device__ __forceinline__ LaneTab lane_tab(int lane, int64_t kstride, int last_row) {
-  LaneTab t;
-  t.n = lane & 31;
-  t.g = lane >> 5;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = 8 * i + (lane >> 3);
-    const int rc = min(r, last_row);
-    const uint32_t c16 = 16u * ((lane & 7) ^ tile_swz(r)) + 3072u - 1024u * i;
-    t.voff[i] = (uint32_t)(r * kstride) + c16;
-    t.voff_last[i] = (uint32_t)(rc * kstride) + c16;
-  }
-  t.kperm = mfma_row_perm(t.n);
-  t.kofs = (uint32_t)(t.kperm * kstride) + 16u * t.g;
-  t.kofs_last = (uint32_t)(min(t.kperm, last_row) * kstride) + 16u * t.g;
-  const int tr_G = lane >> 4, tr_a = (lane >> 2) & 3, tr_b = lane & 3;
-#pragma unroll
-  for (int hf = 0; hf < 2; ++hf)
-#pragma unroll
-    for (int db = 0; db < 2; ++db) {
-      const int row = 8 * (tr_G >> 1) + 4 * hf + tr_a;
-      const int chunk = 4 * db + 2 * (tr_G & 1) + (tr_b >> 1);
-      t.tr_off[hf][db] = row * 128 + ((chunk ^ tile_swz(row)) << 4) + 8 * (tr_b & 1);
-    }
-  return t;
-}
-
-// The lane id from an opaque instruction pair: never merged with an earlier
-// computation of it, so it is formed again instead of kept live.
-__device__ __forceinline__ int fresh_lane_id() {
-  int l;
-  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
-  return l;
-}
+// The per-lane offsets (LaneTab, lane_tab) are formed twice: for the
+// prologue and the key-step loop, and again from a fresh lane id after the
+// loop (for the rerun and the merge), so that no lane-dependent value has to
+// survive the loop, which holds all 256 registers.
 
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 flexrel_w64_kernel(const Params p) {
@@ -580,11 +530,11 @@ flexrel_w64_kernel(const Params p) {
       uint64_t overflow = 0;
 #pragma unroll
       for (int J = 0; J < kBlocks; ++J) overflow |= __builtin_amdgcn_ballot_w64(!(lsum[J][0] < INFINITY));
-      if (__builtin_expect(overflow != 0, 0)) {
-        wait_lgkm0();  // the last V operand reads are done before the rerun refills slot 0
-        continue;
-      }
-      wait_lgkm0();
+      // (The statement returns with every LDS read and copy retired, so its
+      // register outputs -- the V^T operands read below among them -- are
+      // final: a wait placed here in compiled code would not order the
+      // register-only products after it.)
+      if (__builtin_expect(overflow != 0, 0)) continue;
       pv(0, 0);  // PV of items (nu - 1, 0) and (nu - 1, 1)
       pv(1, 1);
       break;

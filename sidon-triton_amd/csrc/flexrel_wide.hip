@@ -642,7 +642,10 @@ flexrel_wide_kernel(const Params p) {
       if (__builtin_expect(overflow != 0, 0)) continue;
       break;
     }
-    wait_lgkm0();
+    // (The statement returns with every LDS read retired, so its register
+    // outputs -- the V^T operands read below among them -- are final: a wait
+    // placed here in compiled code would not order the register-only
+    // products after it.)
     pv(2, 0);  // PV of items (nu - 1, 2) and (nu - 1, 3)
     pv(3, 1);
   }

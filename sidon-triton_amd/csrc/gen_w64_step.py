@@ -43,7 +43,8 @@ from pathlib import Path
 
 sys.path.insert(0, str(Path(__file__).resolve().parent))
 import gen_wide_step as G  # noqa: E402
-from gen_wide_step import Ins, branch, check_hazards, label, mfma16, mfma32, nop, salu, schedule, valu  # noqa: E402
+from gen_wide_step import (Ins, assert_quiet, branch, check_hazards, label, mfma16, mfma32, nop,  # noqa: E402
+                           salu, schedule, valu)
 
 OUT = Path(__file__).resolve().parent / "flexrel_w64_step.inc"
 
@@ -426,10 +427,14 @@ def build():
     sp_text, sp_phases = {}, {}
     for sl in (0, 1):
         sp_text[sl], sp_phases[sl] = special_step(sl, FENCE + pre)
-    # the last block's row sums; every register load has landed before the
-    # compiled code takes the K buffers back
+    # the last block's row sums; then every copy and every LDS read has
+    # retired: the statement's register outputs (the V^T and K operands among
+    # them) are final when it ends.  A wait in the compiled code after it
+    # would not do: the compiler may move register-only work, such as the
+    # last PV products that read the V^T operands, above it.
     tail = [mfma16(rs(1), ("v", SEL), ("v", pk(1, 0)), "R1.end"),
-            mfma16(rs(1), ("v", SEL), ("v", pk(1, 1)), "R2.end"), Ins("s_waitcnt vmcnt(0)", "waitcnt")]
+            mfma16(rs(1), ("v", SEL), ("v", pk(1, 1)), "R2.end"), Ins("s_waitcnt vmcnt(0)", "waitcnt"),
+            Ins("s_waitcnt lgkmcnt(0)", "waitcnt")]
     entry = FENCE + [salu(f"s_movk_i32 s{S_72}, 0x48"), label("L_sp_top_%="),
                      salu(f"s_cmp_ge_i32 s{S_J}, %[nslow]"), branch("s_cbranch_scc1 L_plain_entry_%=")]
     sp_loop = (pre + [salu(f"s_bitcmp1_b32 s{S_J}, 0"), branch("s_cbranch_scc1 L_sp_odd_%=")] + sp_text[0]
@@ -475,6 +480,11 @@ def build():
         seq += pe + (s0 + s1 + s0 if first == 0 else s1 + s0 + s1)
         vm = check_waits(seq, [])
         assert len(vm) <= 8, vm
+    # every exit (after the special steps, after an even or an odd plain
+    # step) leaves nothing in flight
+    for seq in (pe + tail, pe + s0 + advance() + tail, pe + s1 + advance() + tail,
+                pe + s0 + advance() + s1 + advance() + tail):
+        assert_quiet(seq)
     return loop, s0, c0
 
 

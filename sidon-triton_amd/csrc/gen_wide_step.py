@@ -421,6 +421,25 @@ def check_hazards(seq):
             states += p.states()
 
 
+def assert_quiet(seq, copies=True):
+    """Raises unless every LDS read (and, with copies, every copy) issued in
+    seq has retired by its end (whatever was in flight before it, too)."""
+    lds, vm = 99, 99   # (anything in flight before seq counts)
+    for c in seq:
+        if c.kind == "waitcnt":
+            kind, n = c.text.split()[1].split("(")
+            n = int(n.rstrip(")"))
+            if kind == "lgkmcnt":
+                lds = min(lds, n)
+            else:
+                vm = min(vm, n)
+            continue
+        lds += c.kind == "lds"
+        vm += c.kind in ("dma", "gload")
+    if lds or (copies and vm):
+        raise AssertionError(f"{lds} LDS reads / {vm} copies in flight at the end")
+
+
 def check_waits(seq, vm_outstanding):
     """Outstanding-operation check: an LDS read result is used only after an
     lgkmcnt wait retired it, a ring slot is read only after the vmcnt wait
@@ -669,8 +688,12 @@ def build():
     sp_text, sp_phases = {}, {}
     for sl in (0, 1):
         sp_text[sl], sp_phases[sl] = special_step(sl, sp_hist)
+    # the last block's row sums; then every LDS read has retired: the
+    # statement's register outputs (the V^T and K operands among them) are
+    # final when it ends (the compiler may move register-only work after it,
+    # such as the last PV products, above a wait in the compiled code)
     tail = [mfma16(RSACC + 12, ("v", SEL), ("v", pk(1, 0)), "R1.end"),
-            mfma16(RSACC + 12, ("v", SEL), ("v", pk(1, 1)), "R2.end")]
+            mfma16(RSACC + 12, ("v", SEL), ("v", pk(1, 1)), "R2.end"), Ins("s_waitcnt lgkmcnt(0)", "waitcnt")]
     entry = FENCE + [salu(f"s_movk_i32 s{S_72}, 0x48"), label("L_sp_top_%="),
                      salu(f"s_cmp_ge_i32 s{S_J}, %[nslow]"), branch("s_cbranch_scc1 L_plain_entry_%=")]
     sp_loop = (pre + [salu(f"s_bitcmp1_b32 s{S_J}, 0"), branch("s_cbranch_scc1 L_sp_odd_%=")] + sp_text[0]
@@ -717,6 +740,10 @@ def build():
         seq += pe + (s0 + s1 if first == 0 else s1 + s0)
         vm = check_waits(seq, [("K", first), ("V", first), ("K", first ^ 1), ("V", first ^ 1)])
         assert len(vm) <= 12, vm
+    # every exit leaves no LDS read in flight (the copies still in flight
+    # write only LDS, which the compiled code awaits before reusing it)
+    for seq in (pe + tail, pe + e0 + tail, pe + e1 + tail, pe + e0 + e1 + tail):
+        assert_quiet(seq, copies=False)
     return loop, s0, c0
 
 

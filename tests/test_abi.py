@@ -53,9 +53,9 @@ def test_launch_shape(sidon, B, H, L):
     s = sidon._lib.launch_shape(B, H, L)
     qpb = s["queries_per_block"]
     wgs = s["workgroups"]
-    assert qpb in (64, 128)
-    if qpb == 64:
-        assert wgs == B * H * -(-L // 64)
+    assert qpb in (32, 64, 128)
+    if qpb in (32, 64):
+        assert wgs == B * H * -(-L // qpb)
     else:
         assert B * H * -(-L // 128) <= wgs <= B * H * -(-L // 64)
     assert s["threads_per_block"] % 64 == 0
@@ -63,17 +63,28 @@ def test_launch_shape(sidon, B, H, L):
 
 
 def test_shape_choice(sidon, monkeypatch):
-    """The automatic choice is the 64-row kernel with 4 key splits (two
-    workgroups per compute unit) at every length; SIDON_FLEXREL_VARIANT
-    forces another, read at every call.  Without a device the library
-    assumes 256 compute units: forced wide_tail runs c3 (608 blocks of 128
-    rows) as two whole rounds of 128-row blocks and the last 704 rows as
-    64-row blocks."""
+    """The automatic choice: the 32-row kernel (4 key splits) while its
+    workgroups fit one per compute unit, else the 64-row kernel with 4 key
+    splits (two workgroups per compute unit); SIDON_FLEXREL_VARIANT forces
+    another, read at every call.  Without a device the library assumes 256
+    compute units: H = 16 takes the 32-row kernel up to L = 512; forced
+    wide_tail runs c3 (608 blocks of 128 rows) as two whole rounds of
+    128-row blocks and the last 704 rows as 64-row blocks."""
     monkeypatch.delenv("SIDON_FLEXREL_VARIANT", raising=False)
-    for L in (150, 750, 1500, 4800):
+    for L in (150, 500, 512):
+        s = sidon._lib.launch_shape(1, 16, L)
+        assert s["queries_per_block"] == 32 and s["key_splits"] == 4 and s["threads_per_block"] == 256
+        assert s["workgroups"] == 16 * -(-L // 32)
+    for L in (513, 750, 1500, 4800):
         s = sidon._lib.launch_shape(1, 16, L)
         assert s["queries_per_block"] == 64 and s["key_splits"] == 4 and s["threads_per_block"] == 256
         assert s["workgroups"] == 16 * -(-L // 64)
+    assert sidon._lib.launch_shape(2, 16, 300)["queries_per_block"] == 64   # 320 32-row blocks
+    assert sidon._lib.launch_shape(1, 1, 8000)["queries_per_block"] == 32   # 250 32-row blocks
+    monkeypatch.setenv("SIDON_FLEXREL_VARIANT", "w64")
+    assert sidon._lib.launch_shape(1, 16, 150)["queries_per_block"] == 64
+    monkeypatch.setenv("SIDON_FLEXREL_VARIANT", "w32")
+    assert sidon._lib.launch_shape(1, 16, 4800)["workgroups"] == 16 * 150
     monkeypatch.setenv("SIDON_FLEXREL_VARIANT", "wide_tail")
     c3 = sidon._lib.launch_shape(1, 16, 4800)
     assert c3["queries_per_block"] == 128 and c3["workgroups"] == 512 + 16 * 11

@@ -3,8 +3,9 @@ choice (needs an MI355X).
 
 `SIDON_FLEXREL_VARIANT` (read by the library at every call) forces the
 8-split kernel of flexrel_fwd.hip, the 128-row kernel of flexrel_wide.hip
-(alone, and as whole rounds plus an 8-split tail), or the 64-row kernel of
-flexrel_w64.hip; K and V rows of different strides take the 8-split kernel
+(alone, and as whole rounds plus an 8-split tail), the 64-row kernel of
+flexrel_w64.hip or the 32-row kernel of flexrel_w32.hip; K and V rows of
+different strides take the 8-split kernel
 without being forced.  Each is checked against the float64 oracle at the
 north-star bar on ragged and padded shapes, for the same results contract:
 keys past the valid length (refilled with finite garbage, which sends the
@@ -23,7 +24,7 @@ from test_flexrel_gpu import DEV, assert_parity, run
 
 pytestmark = pytest.mark.gpu
 
-VARIANTS = ["split8", "wide", "wide_tail", "w64"]
+VARIANTS = ["split8", "wide", "wide_tail", "w64", "w32"]
 SHAPES = [
     # (B, H, L, lens)
     (1, 2, 33, [20]),
@@ -73,7 +74,7 @@ def test_variant_padding_garbage_bit_identical(sidon, variant):
     assert torch.equal(got[:, :, :LK], got2[:, :, :LK]), f"{variant}: keys past LK changed valid rows"
 
 
-@pytest.mark.parametrize("variant", ["wide_tail", "w64"], indirect=True)
+@pytest.mark.parametrize("variant", ["wide_tail", "w64", "w32"], indirect=True)
 def test_variant_c3_shape(sidon, variant):
     """L=4800, H=16: the grids of several rounds (and the wide kernel's tail launch); 2 heads checked."""
     q, k, v, rel = seeded_inputs(1, 16, 4800, seed=3)
@@ -82,6 +83,58 @@ def test_variant_c3_shape(sidon, variant):
     heads = [0, 15]
     ref = flexrel_reference(q.numpy()[:, heads], k.numpy()[:, heads], v.numpy()[:, heads], rel.numpy())
     assert_parity(ref, got[:, heads], [4800], f"{variant} c3")
+
+
+_FUSED_L3000 = {}
+
+
+def _fused_l3000():
+    """A 60 s chunk in the encoder's fused QKV layout: [L, 3 * 16 * 64] rows
+    of unit-variance values, L = 3000 (the last key step straddles the
+    length); the float64 oracle of all 16 heads, computed once."""
+    if not _FUSED_L3000:
+        L, H = 3000, 16
+        gen = torch.Generator().manual_seed(L)
+        qkv = torch.randn(L, 3 * H * 64, generator=gen).half()
+        rel = (torch.randn(73, 64, generator=gen) * 0.02).half()
+        x = qkv.view(L, 3, H, 64).permute(1, 2, 0, 3).numpy()  # [q|k|v, H, L, 64]
+        ref = flexrel_reference(x[0][None], x[1][None], x[2][None], rel.numpy())[0]  # [H, L, 64]
+        _FUSED_L3000.update(qkv=qkv, rel=rel, ref=ref, L=L, H=H)
+    return _FUSED_L3000
+
+
+@pytest.mark.parametrize("variant", ["w64", "w32"], indirect=True)
+def test_variant_fused_layout_l3000(sidon, variant):
+    c = _fused_l3000()
+    L, H = c["L"], c["H"]
+    lens = torch.tensor([L], dtype=torch.int32, device=DEV)
+    out = sidon.encoder_attention.flexrel_attention(c["qkv"].to(DEV), 1, H, c["rel"].to(DEV), lens)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy().reshape(L, H, 64).transpose(1, 0, 2)[None]
+    assert_parity(c["ref"][None], got, [L], f"{variant} fused L=3000")
+
+
+@pytest.mark.parametrize("variant", ["w64", "wide", "w32"], indirect=True)
+def test_variant_repeated_launches_bit_identical(sidon, variant):
+    """200 launches on the same inputs give the same bits.  Regression test:
+    the hand-scheduled loops once returned with their last V^T operand reads
+    still in flight, and the compiled PV products after the loop (moved by
+    the compiler above the wait meant for them) read stale operands now and
+    then -- one 32-row block's dims 0-31 wrong in ~3% of launches at
+    L = 2990, never at 1500 or 4800."""
+    L, H = 2990, 16
+    gen = torch.Generator().manual_seed(L)
+    qkv = torch.randn(L, 3 * H * 64, generator=gen).half().to(DEV)
+    rel = (torch.randn(73, 64, generator=gen) * 0.02).half().to(DEV)
+    lens = torch.tensor([L], dtype=torch.int32, device=DEV)
+    out = torch.empty(L, H * 64, dtype=torch.float16, device=DEV)
+    first = sidon.encoder_attention.flexrel_attention(qkv, 1, H, rel, lens).clone()
+    bad = 0
+    for _ in range(200):
+        sidon.encoder_attention.flexrel_attention(qkv, 1, H, rel, lens, out=out)
+        bad += int(not torch.equal(out, first))
+    torch.cuda.synchronize()
+    assert bad == 0, f"{variant}: {bad} of 200 launches differ from the first"
 
 
 def test_different_kv_strides_take_the_8_split_kernel(sidon, monkeypatch):

@@ -97,6 +97,26 @@ def test_w64_wait_check_catches_a_missing_copy_wait():
     gen.check_waits(step + step, [])
 
 
+@pytest.mark.parametrize("name", ["gen_wide_step", "gen_w64_step"])
+def test_loop_returns_with_no_lds_read_in_flight(name):
+    """The loop statement's register outputs must be final when it ends: its
+    last V^T and K operand reads are LDS reads, and the compiled code after
+    it may move register-only work (the last PV products) above any wait of
+    its own.  The tail after the L_end label retires every LDS read (and, in
+    the 64-row loop, every copy); dropping that wait must trip the check."""
+    gen = _gen(name)
+    loop, step, _ = gen.build()    # checks every exit path
+    end = max(k for k, ins in enumerate(loop) if ins.text == "L_end_%=:")
+    tail = loop[end + 1:]
+    assert any(ins.text == "s_waitcnt lgkmcnt(0)" for ins in tail)
+    copies = name == "gen_w64_step"
+    read = next(ins for ins in step if ins.kind == "lds")    # an operand read left in flight
+    gen.assert_quiet([read] + tail, copies=copies)
+    planted = [ins for ins in tail if ins.text != "s_waitcnt lgkmcnt(0)"]
+    with pytest.raises(AssertionError, match="in flight at the end"):
+        gen.assert_quiet([read] + planted, copies=copies)
+
+
 def _compiled_loop(src="flexrel_wide.hip"):
     hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not Path(hipcc).exists():
