@@ -73,6 +73,29 @@ int sidon_gemm_bias_act(const void* x, int ldx, const void* w, int ldw, const vo
                         int M, int N, int K, int act, sidon_stream_t stream);
 
 /*
+ * Residual projection, accumulated into the fp32 stream in place:
+ *
+ *   y[m, n] += x[m, :] . w[n, :]        m < M, n < N, fp32 sums
+ *
+ * x [M, K] and w [N, K] fp16 row-major (K contiguous: activations and a torch
+ * Linear weight), y [M, N] fp32 row-major, updated in place.  Replaces the
+ * torch.addmm(x, a, w.t(), out_dtype=torch.float32, out=x) of res(),
+ * src/sidon_triton/triton_encoder.py:491-492.  64 x 64 output tiles, K split
+ * over the workgroup's 4 wavefronts and summed in a fixed order: the result
+ * does not depend on timing.  Shapes: M >= 1, N a multiple of 64, K a
+ * multiple of 128; ldx, ldw multiples of 8 and >= K, ldy a multiple of 4 and
+ * >= N; x, w, y 16-byte aligned.  sidon_gemm_res_fits(M, N, K) says whether
+ * a shape is supported (pure host function); sidon_gemm_res_preferred(M, N,
+ * K) whether the kernel is expected to beat a library GEMM on the current
+ * device (its tiles fit one per compute unit).  Neither has a counterpart in
+ * the reference.
+ */
+int sidon_gemm_res_fits(int M, int N, int K);
+int sidon_gemm_res_preferred(int M, int N, int K);
+int sidon_gemm_res(const void* x, int ldx, const void* w, int ldw, float* y, int ldy, int M, int N, int K,
+                   sidon_stream_t stream);
+
+/*
  * Plain GEMM on rocBLAS with the kernel chosen per problem by timing:
  *
  *   y[m, n] = x[m, :] . w[n, :] + beta * y[m, n]      m < M, n < N, fp32 sums

@@ -10,9 +10,10 @@ type combinations:
     (src/sidon_triton/triton_encoder.py:504);
   * fp16 x, w and an fp32 out, beta 1 -- the form of the residual projections
     of res(), ``torch.addmm(x, a, W^T, out_dtype=float32, out=x)`` (:491-492).
-    The encoder keeps torch.addmm for those: inside its graph rocBLAS's
+    The encoder does not use rocBLAS for those: inside its graph rocBLAS's
     timed choice measured no faster (feed-forward output) or slower (the
-    hidden -> hidden projections).
+    hidden -> hidden projections) than torch.addmm, which it keeps for long
+    chunks, and short chunks take ``conformer.residual_gemm``.
 
 The first call of a problem (shape, strides, types, beta != 0) on a device,
 made while the stream is not capturing, times rocBLAS's kernels for it on

@@ -155,3 +155,42 @@ def linear_silu(x: torch.Tensor, w: torch.Tensor, b: torch.Tensor | None, out: t
                                      1 if act else 0, _stream_handle(device))
     _lib.check("sidon_gemm_bias_act", rc)
     return out
+
+
+def residual_gemm_fits(x: torch.Tensor, a: torch.Tensor, w: torch.Tensor) -> bool:
+    """Whether ``residual_gemm`` takes a [M, K], w [N, K] into x [M, N]."""
+    return (bool(_lib.load().sidon_gemm_res_fits(a.shape[0], w.shape[0], w.shape[1])) and a.shape[1] == w.shape[1]
+            and tuple(x.shape) == (a.shape[0], w.shape[0]))
+
+
+def residual_gemm_preferred(rows: int, n: int, k: int, device=None) -> bool:
+    """Whether ``residual_gemm`` is expected to beat torch.addmm for a
+    [rows, k], w [n, k] on ``device`` (its 64 x 64 tiles fit one per compute
+    unit: rows <= 1024 at n = 1024 on 256 CUs)."""
+    with torch.cuda.device(device):
+        return bool(_lib.load().sidon_gemm_res_preferred(rows, n, k))
+
+
+def residual_gemm(x: torch.Tensor, a: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """x += a . w^T in place: x [M, N] fp32 (the residual stream), a [M, K]
+    and w [N, K] fp16 with K contiguous -- the
+    ``torch.addmm(x, a, w.t(), out_dtype=torch.float32, out=x)`` of the
+    reference's res() (src/sidon_triton/triton_encoder.py:491-492)."""
+    device = x.device
+    for name, t in (("a", a), ("w", w)):
+        _check_device_tensor(name, t, device)
+        if t.dtype != torch.float16 or t.dim() != 2 or t.stride(1) != 1:
+            raise ValueError(f"{name} must be a float16 [rows, K] tensor with K contiguous")
+    _check_device_tensor("x", x, device)
+    rows, k = a.shape
+    n = w.shape[0]
+    if w.shape[1] != k:
+        raise ValueError(f"a has {k} columns, w {w.shape[1]}")
+    if x.dtype != torch.float32 or tuple(x.shape) != (rows, n) or x.stride(1) != 1:
+        raise ValueError(f"x must be a float32 [{rows}, {n}] tensor with rows contiguous")
+    lib = _lib.load()
+    with torch.cuda.device(device):
+        rc = lib.sidon_gemm_res(a.data_ptr(), a.stride(0), w.data_ptr(), w.stride(0), x.data_ptr(), x.stride(0),
+                                rows, n, k, _stream_handle(device))
+    _lib.check("sidon_gemm_res", rc)
+    return x

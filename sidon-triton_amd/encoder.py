@@ -16,9 +16,10 @@ Mirrors src/sidon_triton/triton_encoder.py:
     ``load_encoder`` also reads the reference's own ``encoder_triton.pt``
     (with ``torch.load(weights_only=True)``).
 
-Per layer the work is: res_norm (HIP), hipBLASLt GEMMs through torch (QKV,
-the residual projections), the pointwise conv's first GEMM on rocBLAS with
-the kernel chosen by timing (``blas.gemm_nt``), the
+Per layer the work is: res_norm (HIP), the QKV GEMM on hipBLASLt through
+torch, the residual projections into the fp32 stream (one HIP kernel while
+its 64 x 64 tiles fit one per CU, else hipBLASLt), the pointwise conv's first
+GEMM on rocBLAS with the kernel chosen by timing (``blas.gemm_nt``), the
 feed-forward input projections with bias and SiLU (one HIP GEMM kernel where
 its tiles fill the chip, else hipBLASLt followed by the in-place HIP SiLU),
 the relative_key attention (HIP), and the conv module's GLU + causal
@@ -36,7 +37,8 @@ from pathlib import Path
 import torch
 
 from .blas import gemm_nt
-from .conformer import glu_causal_dw_norm, linear_silu, linear_silu_preferred, silu_
+from .conformer import (glu_causal_dw_norm, linear_silu, linear_silu_preferred, residual_gemm,
+                        residual_gemm_preferred, silu_)
 from .encoder_attention import flexrel_attention
 from .encoder_block import res_norm
 from .flexrel import HEAD_DIM, LEFT, NUM_POS, RIGHT
@@ -155,10 +157,13 @@ class HipEncoder:
     """fp32 features [B, L, F] (+ valid frames [B]) -> hidden [B, L, C] fp32 on
     packed weights (``pack_encoder`` / ``pack_weights``)."""
 
-    def __init__(self, packed: dict, device="cuda", fused_ffn: bool | None = None) -> None:
+    def __init__(self, packed: dict, device="cuda", fused_ffn: bool | None = None,
+                 own_residual: bool | None = None) -> None:
         """fused_ffn: the feed-forward input projections as one GEMM + bias +
         SiLU kernel (True), as hipBLASLt + SiLU (False), or chosen per call
-        by shape (None)."""
+        by shape (None).  own_residual: the residual projections on this
+        library's kernel (True, ``conformer.residual_gemm``), on torch.addmm
+        (False), or chosen per call by shape (None)."""
         device = torch.device(device)
         if device.type == "cuda" and device.index is None:
             device = torch.device("cuda", torch.cuda.current_device())
@@ -172,6 +177,7 @@ class HipEncoder:
         self.features = self.fp_w.shape[1]
         self.inter = self.layers[0]["ffn1_w1"].shape[0]
         self.fused_ffn = fused_ffn
+        self.own_residual = own_residual
 
     def workspace(self, rows: int) -> dict:
         """Buffers for calls of up to ``rows`` = B*L rows (graph capture
@@ -230,11 +236,17 @@ class HipEncoder:
                 return linear_silu(xn, w, b, out=h_buf)
             return silu_(torch.addmm(b, xn, w.t(), out=h_buf))
 
+        own = {k: (residual_gemm_preferred(rows, hid, k, device) if self.own_residual is None
+                   else self.own_residual) for k in (hid, self.inter)}
+
         def res(a, w, bias, **kw):
-            # The residual projections stay on torch.addmm (hipBLASLt): inside
-            # the encoder graph rocBLAS's timed choice was no faster for the
-            # feed-forward output and slower for the hid -> hid projections.
-            torch.addmm(x, a, w.t(), out_dtype=torch.float32, out=x)
+            # The residual projections: this library's kernel while its 64 x 64
+            # tiles fit one per CU (short chunks), else torch.addmm (hipBLASLt);
+            # rocBLAS's timed choice was no faster inside the encoder graph.
+            if own[a.shape[1]]:
+                residual_gemm(x, a, w)
+            else:
+                torch.addmm(x, a, w.t(), out_dtype=torch.float32, out=x)
             return res_norm(x, bias=bias, xn=xn_buf if kw.get("norm2") is not None else None, **kw)
 
         for i, p in enumerate(layers):

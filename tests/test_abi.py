@@ -181,6 +181,38 @@ def test_gemm_rejects_bad_arguments_before_launch(sidon, over, code):
     assert lib.sidon_last_error().decode()
 
 
+def test_residual_gemm_shape_support(sidon):
+    lib = sidon._lib.load()
+    assert lib.sidon_gemm_res_fits(750, 1024, 4096) == 1
+    assert lib.sidon_gemm_res_fits(1, 64, 128) == 1
+    for m, n, k in ((0, 1024, 1024), (750, 1000, 1024), (750, 32, 1024), (750, 1024, 1000), (750, 1024, 64)):
+        assert lib.sidon_gemm_res_fits(m, n, k) == 0, (m, n, k)
+
+
+@pytest.mark.parametrize("over,code", [
+    (dict(x=None), -1),
+    (dict(w=None), -1),
+    (dict(y=None), -1),
+    (dict(N=1000), -2),
+    (dict(K=1000), -2),
+    (dict(M=0), -2),
+    (dict(ldx=1000), -3),
+    (dict(ldw=1020), -3),
+    (dict(ldy=1026), -3),
+    (dict(x=24), -4),
+    (dict(y=40), -4),
+])
+def test_residual_gemm_rejects_bad_arguments_before_launch(sidon, over, code):
+    # fake aligned addresses, never dereferenced: validation returns before any HIP call
+    lib = sidon._lib.load()
+    args = dict(x=16, ldx=1024, w=16, ldw=1024, y=16, ldy=1024, M=750, N=1024, K=1024)
+    args.update(over)
+    rc = lib.sidon_gemm_res(args["x"], args["ldx"], args["w"], args["ldw"], args["y"], args["ldy"], args["M"],
+                            args["N"], args["K"], None)
+    assert rc == code
+    assert lib.sidon_last_error().decode()
+
+
 # The encoder and front-end entry points, the same way: fake aligned addresses
 # that are never dereferenced, each case wrong in exactly one argument, so
 # validation returns before any HIP call.  (No case is valid: on a GPU box a

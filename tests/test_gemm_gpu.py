@@ -145,3 +145,58 @@ def test_runtime_full_chunk_graph_replays_match_eager(sidon):
         assert torch.equal(got[0, :frames], want[0, :frames]), rep
         _ = (want * 2).sum().item()  # unrelated eager work between replays
     assert len(rt.graphs) == 1
+
+
+# ---- the residual projection into the fp32 stream (csrc/gemm_res.hip) ----
+
+@pytest.mark.parametrize("m,n,k,ldx,ldy", [
+    (750, 1024, 4096, None, None),
+    (750, 1024, 1024, None, None),
+    (1500, 1024, 1024, None, None),
+    (63, 64, 128, None, None),
+    (1, 128, 256, None, None),
+    (333, 192, 384, 400, 200),
+])
+def test_residual_gemm_matches_fp32(sidon, m, n, k, ldx, ldy):
+    """x += a . w^T against float64 on the CPU from the same fp16 inputs and
+    fp32 stream; columns past N and rows past M of a wider / taller stream
+    buffer are left untouched; two calls from the same state give the same
+    bits."""
+    gen = torch.Generator().manual_seed(m + n + k)
+    ldx = k if ldx is None else ldx
+    ldy = n if ldy is None else ldy
+    a_full = torch.randn(m, ldx, generator=gen).half()
+    a = a_full[:, :k]
+    w = (torch.randn(n, k, generator=gen) / k ** 0.5).half()
+    x0 = torch.randn(m + 3, ldy, generator=gen)
+    ref = x0.double().clone()
+    ref[:m, :n] += a.double() @ w.double().t()
+    buf = x0.to(DEV)
+    x = buf[:m, :n]
+    a_d, w_d = a_full.to(DEV)[:, :k], w.to(DEV)   # a keeps its row stride ldx on the device
+    assert a_d.stride(0) == ldx
+    got = sidon.conformer.residual_gemm(x, a_d, w_d)
+    assert got.data_ptr() == x.data_ptr()
+    out = buf.cpu()
+    assert torch.equal(out[m:], x0[m:]) and torch.equal(out[:m, n:], x0[:m, n:])
+    err = (out[:m, :n].double() - ref[:m, :n]).abs()
+    # fp32 sums of k products: a few fp32 roundings of the running sum
+    tol = 1e-5 * (1 + ref[:m, :n].abs()) * max(1.0, (k / 1024) ** 0.5)
+    assert (err <= tol).all(), float(err.max())
+    again = x0.to(DEV)
+    sidon.conformer.residual_gemm(again[:m, :n], a_d, w_d)
+    assert torch.equal(again.cpu(), out)
+
+
+def test_residual_gemm_matches_addmm(sidon):
+    """The encoder's feed-forward output at a 15 s chunk against the
+    torch.addmm(x, a, w.t(), out_dtype=float32) it replaces: the same fp32
+    sums in another order."""
+    gen = torch.Generator().manual_seed(5)
+    a = torch.randn(750, 4096, generator=gen).half().to(DEV)
+    w = (torch.randn(1024, 4096, generator=gen) / 64).half().to(DEV)
+    x = torch.randn(750, 1024, generator=gen).to(DEV)
+    ref = torch.addmm(x, a, w.t(), out_dtype=torch.float32)
+    got = sidon.conformer.residual_gemm(x.clone(), a, w)
+    torch.cuda.synchronize()
+    assert float((got - ref).abs().max()) <= 1e-4
