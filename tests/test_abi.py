@@ -187,6 +187,7 @@ def test_residual_gemm_shape_support(sidon):
     assert lib.sidon_gemm_res_fits(1, 64, 128) == 1
     for m, n, k in ((0, 1024, 1024), (750, 1000, 1024), (750, 32, 1024), (750, 1024, 1000), (750, 1024, 64)):
         assert lib.sidon_gemm_res_fits(m, n, k) == 0, (m, n, k)
+        assert lib.sidon_gemm_res_preferred(m, n, k) == 0, (m, n, k)   # unsupported: never preferred
 
 
 @pytest.mark.parametrize("over,code", [
