@@ -330,7 +330,7 @@ SIDON_API int sidon_gemm_nt_tune(const void* x, int ldx, const void* w, int ldw,
 
   hipEvent_t e0 = nullptr, e1 = nullptr;
   if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) {
-    if (e0) hipEventDestroy(e0);
+    if (e0) (void)hipEventDestroy(e0);
     return fail(SIDON_E_LAUNCH, "hipEventCreate failed");
   }
   // Each candidate: two untimed runs, then the best of two timed groups of
@@ -340,17 +340,17 @@ SIDON_API int sidon_gemm_nt_tune(const void* x, int ldx, const void* w, int ldw,
     bool ok = run(h, p, c) == rocblas_status_success && run(h, p, c) == rocblas_status_success;
     float us = 1e30f;
     for (int rep = 0; ok && rep < 2; ++rep) {
-      hipEventRecord(e0, s);
+      ok = ok && hipEventRecord(e0, s) == hipSuccess;
       for (int i = 0; i < 4; ++i) ok = ok && run(h, p, c) == rocblas_status_success;
-      hipEventRecord(e1, s);
+      ok = ok && hipEventRecord(e1, s) == hipSuccess;
       float ms = 0.f;
-      if (hipEventSynchronize(e1) != hipSuccess || hipEventElapsedTime(&ms, e0, e1) != hipSuccess) ok = false;
+      if (!ok || hipEventSynchronize(e1) != hipSuccess || hipEventElapsedTime(&ms, e0, e1) != hipSuccess) ok = false;
       if (ms * 250.f < us) us = ms * 250.f;  // 1000 us / 4 calls
     }
     if (ok) timed.emplace_back(us, c);
   }
-  hipEventDestroy(e0);
-  hipEventDestroy(e1);
+  (void)hipEventDestroy(e0);  // (nothing to do if destroying fails)
+  (void)hipEventDestroy(e1);
   std::sort(timed.begin(), timed.end());
   // Accuracy gate (agrees()): the fastest candidate whose product agrees with
   // the default's at beta = 0 and, for a problem with beta != 0, also with

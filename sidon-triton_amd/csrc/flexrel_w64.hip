@@ -502,6 +502,11 @@ flexrel_w64_kernel(const Params p) {
       const uint32_t qbase_lds = (uint32_t)(uintptr_t)SIDON_LDS_PTR(float, qr_tab + n * kQrStride);
       const int laned = 8 * g - n;
       const int g8 = 8 * g;
+      // (The loop writes M0 for its LDS copies; the clobber says so.  The
+      // compiler treats M0 as reserved and warns; no compiled code of these
+      // kernels relies on M0 across the statement.)
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
       asm volatile(SIDON_W64_LOOP
                    : "+{v[0:15]}"(oacc[0][0]), "+{v[16:31]}"(oacc[0][1]), "+{v[32:47]}"(oacc[1][0]),
                      "+{v[48:63]}"(oacc[1][1]), "+{v[64:79]}"(sacc[0]), "+{v[80:95]}"(sacc[1]),
@@ -527,6 +532,7 @@ flexrel_w64_kernel(const Params p) {
                      [tv10] "v"(tv[1][0]), [tv11] "v"(tv[1][1]), [qbase] "v"(qbase_lds), [laned] "v"(laned),
                      [g8] "v"(g8)
                    : SIDON_W64_VGPR_CLOBBERS, SIDON_W64_SGPR_CLOBBERS, "vcc", "m0", "scc", "memory");
+#pragma clang diagnostic pop
       uint64_t overflow = 0;
 #pragma unroll
       for (int J = 0; J < kBlocks; ++J) overflow |= __builtin_amdgcn_ballot_w64(!(lsum[J][0] < INFINITY));
