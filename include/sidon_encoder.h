@@ -84,7 +84,7 @@ int sidon_gemm_bias_act(const void* x, int ldx, const void* w, int ldw, const vo
  * over the workgroup's 4 wavefronts and summed in a fixed order: the result
  * does not depend on timing.  Shapes: M >= 1, N a multiple of 64, K a
  * multiple of 128; ldx, ldw multiples of 8 and >= K, ldy a multiple of 4 and
- * >= N; x, w, y 16-byte aligned.  sidon_gemm_res_fits(M, N, K) says whether
+ * >= N; x, w, y 16-byte aligned; x and w must not overlap y.  sidon_gemm_res_fits(M, N, K) says whether
  * a shape is supported (pure host function); sidon_gemm_res_preferred(M, N,
  * K) whether the kernel is expected to beat a library GEMM on the current
  * device (its tiles fit one per compute unit).  Neither has a counterpart in
