@@ -755,23 +755,29 @@ int forced_variant() {
   return -1;
 }
 
-// Automatic choice, from launch timings on MI355X (B = 1, H = 16,
-// L = 150 .. 4800): when the 32-row kernel's workgroups (B H ceil(L / 32))
-// fit one per compute unit, it is the fastest (its critical path -- q.rel
-// table, steps near the diagonal, merge -- is half the 64-row kernel's, and
-// no workgroup shares a compute unit); above that, the two-workgroups-per-CU
-// 64-row kernel is the fastest or level with the fastest at every length
-// (its key-step loop keeps the matrix core busy with two wavefronts per
-// SIMD; the 32-row kernel's pairs contend in their latency-bound phases, the
-// 8-split kernel's steps cost more, the 128-row kernel's blocks are too few
-// below a full round of the chip).  K and V rows of different strides take
-// the 8-split kernel.
+// Automatic choice, from launch timings on MI355X (B = 1; H = 16 at
+// L = 150 .. 4800, H = 1, 4, 8 at L = 512 .. 8000): when the 32-row kernel's
+// workgroups (B H ceil(L / 32)) fit one per compute unit and the keys are
+// few (L <= 1024), it is the fastest (its fixed costs -- q.rel table, steps
+// near the diagonal, merge -- are half the 64-row kernel's, and no
+// workgroup shares a compute unit; its compiled one-block step costs more
+// than the 64-row kernel's hand-scheduled two-block step, so long key
+// ranges favour the 64-row kernel whatever the grid: H = 1, L = 8000: 48.9
+// against 35.1 us; H = 4, L = 2048: 16.3 against 14.6 us; H = 8, L = 1024:
+// 10.6 against 11.2 us; H = 8, L = 600: 8.2 against 10.4 us).
+// Otherwise the two-workgroups-per-CU 64-row kernel is the fastest or level
+// with the fastest at every length (its key-step loop keeps the matrix core
+// busy with two wavefronts per SIMD; the 32-row kernel's pairs contend in
+// their latency-bound phases, the 8-split kernel's steps cost more, the
+// 128-row kernel's blocks are too few below a full round of the chip).  K
+// and V rows of different strides take the 8-split kernel.
+constexpr int kW32MaxKeys = 1024;
 Variant choose_variant(int B, int H, int L, bool same_stride) {
   if (!same_stride) return kSplit8;  // the other kernels are built for K and V rows of one stride
   const int f = forced_variant();
   if (f >= 0) return (Variant)f;
   const long long w32_blocks = (long long)B * H * ((L + w32_rows() - 1) / w32_rows());
-  return w32_blocks <= sidon::compute_units() ? kW32 : kW64;
+  return L <= kW32MaxKeys && w32_blocks <= sidon::compute_units() ? kW32 : kW64;
 }
 
 // One launch: `rows` query rows per workgroup, nqb blocks per (b, h) from

@@ -64,9 +64,11 @@ def test_launch_shape(sidon, B, H, L):
 
 def test_shape_choice(sidon, monkeypatch):
     """The automatic choice: the 32-row kernel (4 key splits) while its
-    workgroups fit one per compute unit, else the 64-row kernel with 4 key
+    workgroups fit one per compute unit and L <= 512, else the 64-row kernel with 4 key
     splits (two workgroups per compute unit); SIDON_FLEXREL_VARIANT forces
-    another, read at every call.  Without a device the library assumes 256
+    another, read at every call.  The 32-row kernel also needs L <= 1024 (its
+    compiled key steps cost more than the 64-row kernel's hand-scheduled ones).
+    Without a device the library assumes 256
     compute units: H = 16 takes the 32-row kernel up to L = 512; forced
     wide_tail runs c3 (608 blocks of 128 rows) as two whole rounds of
     128-row blocks and the last 704 rows as 64-row blocks."""
@@ -80,7 +82,10 @@ def test_shape_choice(sidon, monkeypatch):
         assert s["queries_per_block"] == 64 and s["key_splits"] == 4 and s["threads_per_block"] == 256
         assert s["workgroups"] == 16 * -(-L // 64)
     assert sidon._lib.launch_shape(2, 16, 300)["queries_per_block"] == 64   # 320 32-row blocks
-    assert sidon._lib.launch_shape(1, 1, 8000)["queries_per_block"] == 32   # 250 32-row blocks
+    assert sidon._lib.launch_shape(1, 4, 512)["queries_per_block"] == 32    # 64 32-row blocks
+    assert sidon._lib.launch_shape(1, 1, 8000)["queries_per_block"] == 64   # 250 blocks, but 63 steps a wavefront
+    assert sidon._lib.launch_shape(1, 4, 1024)["queries_per_block"] == 32   # 128 blocks
+    assert sidon._lib.launch_shape(1, 4, 1025)["queries_per_block"] == 64
     monkeypatch.setenv("SIDON_FLEXREL_VARIANT", "w64")
     assert sidon._lib.launch_shape(1, 16, 150)["queries_per_block"] == 64
     monkeypatch.setenv("SIDON_FLEXREL_VARIANT", "w32")
