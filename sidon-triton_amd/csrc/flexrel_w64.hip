@@ -529,7 +529,7 @@ flexrel_w64_kernel(const Params p) {
                      [ko1] "v"(lt.voff[1]), [ko2] "v"(lt.voff[2]), [ko3] "v"(lt.voff[3]), [kl0] "v"(lt.voff_last[0]),
                      [kl1] "v"(lt.voff_last[1]), [kl2] "v"(lt.voff_last[2]), [kl3] "v"(lt.voff_last[3]),
                      [ka0] "v"(ka[0]), [ka1] "v"(ka[1]), [ka2] "v"(ka[2]), [ka3] "v"(ka[3]), [tv00] "v"(tv[0][0]), [tv01] "v"(tv[0][1]),
-                     [tv10] "v"(tv[1][0]), [tv11] "v"(tv[1][1]), [qbase] "v"(qbase_lds), [laned] "v"(laned),
+                     [tv10] "v"(tv[1][0]), [tv11] "v"(tv[1][1]), [qbase] "v"(qbase_lds), [qhi] "v"(qbase_lds + 4 * (kNumPos - 1)), [laned] "v"(laned),
                      [g8] "v"(g8)
                    : SIDON_W64_VGPR_CLOBBERS, SIDON_W64_SGPR_CLOBBERS, "vcc", "m0", "scc", "memory");
 #pragma clang diagnostic pop

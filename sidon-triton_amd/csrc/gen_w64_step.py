@@ -56,7 +56,7 @@ V_SLOT, K_SLOT = 16384, 32768   # LDS offsets of V slot 1 and of the K slot from
 NB, NBR = 124, 126
 S_J, S_NU, S_JUMP, S_RING, S_SCALE, S_T = 64, 65, 66, 67, 68, 69
 S_GK, S_GV, S_DSTEP, S_DJUMP, S_D = 70, 72, 74, 76, 78
-S_GEN, S_MSK, S_NEEDY, S_DU, S_LIM, S_72 = 80, 81, 82, 83, 85, 86   # S_DU: two
+S_GEN, S_MSK, S_NEEDY, S_DU, S_LIM = 80, 81, 82, 83, 85   # S_DU: two
 S_TMP = 87        # s87..s95
 QR_BLOCK = 32 * 76 * 4
 VGPR_CLOBBERS = [f"v{r}" for r in range(T0, X0 + 5)]
@@ -173,18 +173,23 @@ def key_col(i):
 
 
 def gather_valu(J):
-    out = [valu(f"v_add_u32_e32 {x(0)}, s{S_DU + J}, %[laned]", (), {x(0)}, f"D.{J}")]
+    """LDS reads of the 16 biases of a band item: byte address = the lane's
+    q.rel row (qbase) + 4 (d0 + key column), clamped to [qbase, qhi] =
+    [qbase, qbase + 4 * 72] by one v_med3 (the clamp of the position to
+    [0, 72]): two vector instructions per bias."""
+    d = valu(f"v_add_u32_e32 {x(0)}, s{S_DU + J}, %[laned]", (), {x(0)}, f"D.{J}")
+    b = valu(f"v_lshl_add_u32 {x(0)}, {x(0)}, 2, %[qbase]", {x(0)}, {x(0)}, f"B.{J}")
+    b.deps = [d.tag]
+    out = [d, b]
     for i in range(16):
-        a = valu(f"v_add_u32_e32 {t(i)}, {key_col(i)}, {x(0)}", {x(0)}, {t(i)}, f"A{i}.{J}")
-        a.deps = [f"D.{J}"]
-        m = valu(f"v_med3_i32 {t(i)}, {t(i)}, 0, s{S_72}", {t(i)}, {t(i)}, f"M{i}.{J}")
+        a = valu(f"v_add_u32_e32 {t(i)}, {4 * key_col(i)}, {x(0)}", {x(0)}, {t(i)}, f"A{i}.{J}")
+        a.deps = [b.tag]
+        m = valu(f"v_med3_i32 {t(i)}, {t(i)}, %[qbase], %[qhi]", {t(i)}, {t(i)}, f"M{i}.{J}")
         m.deps = [a.tag]
-        sh = valu(f"v_lshl_add_u32 {t(i)}, {t(i)}, 2, %[qbase]", {t(i)}, {t(i)}, f"S{i}.{J}")
-        sh.deps = [m.tag]
         rd = Ins(f"ds_read_b32 {t(i)}, {t(i)} offset:{QR_BLOCK * J}", "lds", reads={t(i)}, writes={t(i)},
                  tag=f"G{i}.{J}")
-        rd.deps = [sh.tag]
-        out += [a, m, sh, rd]
+        rd.deps = [m.tag]
+        out += [a, m, rd]
     return out
 
 
@@ -435,7 +440,7 @@ def build():
     tail = [mfma16(rs(1), ("v", SEL), ("v", pk(1, 0)), "R1.end"),
             mfma16(rs(1), ("v", SEL), ("v", pk(1, 1)), "R2.end"), Ins("s_waitcnt vmcnt(0)", "waitcnt"),
             Ins("s_waitcnt lgkmcnt(0)", "waitcnt")]
-    entry = FENCE + [salu(f"s_movk_i32 s{S_72}, 0x48"), label("L_sp_top_%="),
+    entry = FENCE + [label("L_sp_top_%="),
                      salu(f"s_cmp_ge_i32 s{S_J}, %[nslow]"), branch("s_cbranch_scc1 L_plain_entry_%=")]
     sp_loop = (pre + [salu(f"s_bitcmp1_b32 s{S_J}, 0"), branch("s_cbranch_scc1 L_sp_odd_%=")] + sp_text[0]
                + [salu(f"s_add_u32 s{S_J}, s{S_J}, 1"), branch("s_branch L_sp_top_%="), label("L_sp_odd_%=")]
