@@ -226,44 +226,46 @@ flexrel_w64_kernel(const Params p) {
     }
   }
 
-  // q.rel^T * scale for the 64 rows: six (32 positions x 32 rows) tiles
-  // rel . Q^T; wavefronts 0 and 1 take position blocks 0 and 1 of row block
-  // w, wavefronts 2 and 3 position block 2 of row block w - 2.  Rel rows >= 73
-  // are 0.
-  const int rb = w & 1;
-  const int npb = w < 2 ? 2 : 1;
+  // q.rel^T * scale for the 64 rows, as twenty (16 positions x 16 rows)
+  // tiles rel . Q^T of v_mfma_f32_16x16x32_f16: wavefront w takes rows
+  // 16 w + [0, 16) and all five position blocks (positions 0-79; rel rows
+  // >= 73 are 0, positions >= 76 are not stored) -- five independent
+  // two-product chains per wavefront.  Lane l supplies position (A) and row
+  // (B) l % 16, dims 32 t + 8 (l / 16) + [0, 8) of k-step t, and receives
+  // positions 4 (l / 16) + [0, 4) of row l % 16.
   float* qr_tab = reinterpret_cast<float*>(smem + kQrOff);
   {
-    const int r = 32 * rb + n;
-    h8 qw[4];
+    const int c16 = lane & 15, kg = lane >> 4;
+    const int qr = 16 * w + c16;
+    h8 qb[2];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      // (selected by value: a select between the two arrays would become a
-      // pointer select through scratch memory)
-      const h8 a0 = qop[0][s], a1 = qop[1][s];
-      qw[s] = rb ? a1 : a0;
+    for (int t = 0; t < 2; ++t) {
+      const int c = 4 * t + kg;
+      qb[t] = *reinterpret_cast<const h8*>(smem + kQStageOff + qr * 128 + ((c ^ tile_swz(qr)) << 4));
+      if (q0 + qr >= p.L) qb[t] = h8{};
+    }
+    f32x4 acc[5];
+#pragma unroll
+    for (int pb = 0; pb < 5; ++pb) {
+      const int pos = 16 * pb + c16;
+      const int r2 = min(pos - 64, 15);
+      acc[pb] = f32x4{};
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int c = 4 * t + kg;
+        const char* src = pb < 4 ? smem + kRelOff + pos * 128 + ((c ^ tile_swz(pos)) << 4)
+                                 : smem + kRel2Off + r2 * 128 + ((c ^ tile_swz(r2)) << 4);
+        h8 e = *reinterpret_cast<const h8*>(src);
+        if (pos >= kNumPos) e = h8{};
+        acc[pb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(e, qb[t], acc[pb], 0, 0, 0);
+      }
     }
 #pragma unroll
-    for (int pi = 0; pi < 2; ++pi) {
-      if (pi >= npb) break;
-      const int pb = w < 2 ? pi : 2;
-      const int pos = 32 * pb + n;
-      const char* rrow = pb < 2 ? smem + kRelOff + pb * kTile + n * 128 : smem + kRel2Off + min(n, 15) * 128;
-      f32x16 acc = {};
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        h8 e = *reinterpret_cast<const h8*>(rrow + (((2 * s + g) ^ tile_swz(n)) << 4));
-        if (pos >= kNumPos) e = h8{};
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(e, qw[s], acc, 0, 0, 0);
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int pos0 = 32 * pb + 8 * i + 4 * g;
-        if (pos0 < kQrStride) {
-          const f4 val = {acc[4 * i] * scale, acc[4 * i + 1] * scale, acc[4 * i + 2] * scale,
-                          acc[4 * i + 3] * scale};
-          *reinterpret_cast<f4*>(qr_tab + r * kQrStride + pos0) = val;
-        }
+    for (int pb = 0; pb < 5; ++pb) {
+      const int pos0 = 16 * pb + 4 * kg;
+      if (pos0 < kQrStride) {
+        const f4 val = {acc[pb][0] * scale, acc[pb][1] * scale, acc[pb][2] * scale, acc[pb][3] * scale};
+        *reinterpret_cast<f4*>(qr_tab + qr * kQrStride + pos0) = val;
       }
     }
   }
