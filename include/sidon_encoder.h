@@ -73,6 +73,27 @@ int sidon_gemm_bias_act(const void* x, int ldx, const void* w, int ldw, const vo
                         int M, int N, int K, int act, sidon_stream_t stream);
 
 /*
+ * The same projection on hipBLASLt, for the shapes where the kernel above
+ * leaves CUs idle:
+ *
+ *   y[m, n] = act(x[m, :] . w[n, :] + bias[n])     act: 1 = SiLU, 0 = none
+ *
+ * x [M, K], w [N, K] fp16 (row strides ldx, ldw; K-contiguous), fp32 sums,
+ * bias fp16 [N] or NULL, y [M, N] fp16 (row stride ldy).  The bias and the
+ * SiLU run in hipBLASLt's epilogue on the fp32 sum, with one rounding to
+ * fp16 (the kernel above and the reference round the biased sum to fp16
+ * before the SiLU: the two differ by at most about one fp16 ulp).  Replaces
+ * the torch.addmm(b1, xn, W1^T) + in-place F.silu pair of
+ * src/sidon_triton/triton_encoder.py:498-499 and :507-508.  Shapes: M, N,
+ * K >= 1, strides >= the row lengths, every operand 2-byte aligned.  The
+ * kernel is hipBLASLt's first heuristic choice that needs no workspace,
+ * kept per problem; the first call on a device creates its hipBLASLt handle
+ * and must not run during stream capture.
+ */
+int sidon_gemm_lt_act(const void* x, int ldx, const void* w, int ldw, const void* bias, void* y, int ldy, int M,
+                      int N, int K, int act, sidon_stream_t stream);
+
+/*
  * Residual projection, accumulated into the fp32 stream in place:
  *
  *   y[m, n] += x[m, :] . w[n, :]        m < M, n < N, fp32 sums

@@ -41,6 +41,8 @@ SIGNATURES = {
     "sidon_gemm_bias_act_preferred": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int]),
     "sidon_gemm_bias_act": (ctypes.c_int, [_VP, ctypes.c_int, _VP, ctypes.c_int, _VP, _VP, ctypes.c_int,
                                            ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _VP]),
+    "sidon_gemm_lt_act": (ctypes.c_int, [_VP, ctypes.c_int, _VP, ctypes.c_int, _VP, _VP, ctypes.c_int,
+                                         ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _VP]),
     "sidon_gemm_res_fits": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int]),
     "sidon_gemm_res_preferred": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int]),
     "sidon_gemm_res": (ctypes.c_int, [_VP, ctypes.c_int, _VP, ctypes.c_int, _VP, ctypes.c_int, ctypes.c_int,

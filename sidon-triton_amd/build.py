@@ -18,10 +18,10 @@ PKG_DIR = Path(__file__).resolve().parent
 REPO_DIR = PKG_DIR.parent
 LIB_NAME = "libsidon_flexrel.so"
 SOURCES = [PKG_DIR / "csrc" / name
-           for name in ("flexrel_fwd.hip", "flexrel_wide.hip", "flexrel_w64.hip", "flexrel_w32.hip", "res_norm.hip", "conformer_ops.hip", "fbank.hip", "gemm.hip", "gemm_res.hip", "blas.hip")]
+           for name in ("flexrel_fwd.hip", "flexrel_wide.hip", "flexrel_w64.hip", "flexrel_w32.hip", "res_norm.hip", "conformer_ops.hip", "fbank.hip", "gemm.hip", "gemm_res.hip", "blas.hip", "blaslt.hip")]
 # rocBLAS for the plain GEMMs of csrc/blas.hip.  Its soname is the one torch
 # bundles, so inside a torch process the library shares torch's copy.
-LIBS = ["-lrocblas"]
+LIBS = ["-lrocblas", "-lhipblaslt"]
 ARCH = "gfx950"
 
 # -packed-fp32-ops: no v_pk_{add,mul,fma}_f32 in the generated code.

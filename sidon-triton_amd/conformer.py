@@ -125,10 +125,7 @@ def linear_silu_preferred(rows: int, n: int, k: int, device=None) -> bool:
         return bool(_lib.load().sidon_gemm_bias_act_preferred(rows, n, k))
 
 
-def linear_silu(x: torch.Tensor, w: torch.Tensor, b: torch.Tensor | None, out: torch.Tensor | None = None,
-                act: bool = True) -> torch.Tensor:
-    """silu(fp16(x . w^T + b)) [M, N] fp16 for x [M, K] and w [N, K] fp16
-    (rows K-contiguous), b [N] fp16 or None; act=False leaves out the SiLU."""
+def _linear_args(x: torch.Tensor, w: torch.Tensor, b: torch.Tensor | None, out: torch.Tensor | None):
     device = x.device
     for name, t in (("x", x), ("w", w)):
         _check_device_tensor(name, t, device)
@@ -148,12 +145,39 @@ def linear_silu(x: torch.Tensor, w: torch.Tensor, b: torch.Tensor | None, out: t
         _check_device_tensor("out", out, device)
         if out.dtype != torch.float16 or tuple(out.shape) != (rows, n) or out.stride(1) != 1:
             raise ValueError(f"out must be a float16 [{rows}, {n}] tensor with rows contiguous")
+    return rows, n, k, out
+
+
+def linear_silu(x: torch.Tensor, w: torch.Tensor, b: torch.Tensor | None, out: torch.Tensor | None = None,
+                act: bool = True) -> torch.Tensor:
+    """silu(fp16(x . w^T + b)) [M, N] fp16 for x [M, K] and w [N, K] fp16
+    (rows K-contiguous), b [N] fp16 or None; act=False leaves out the SiLU."""
+    device = x.device
+    rows, n, k, out = _linear_args(x, w, b, out)
     lib = _lib.load()
     with torch.cuda.device(device):
         rc = lib.sidon_gemm_bias_act(x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0),
                                      None if b is None else b.data_ptr(), out.data_ptr(), out.stride(0), rows, n, k,
                                      1 if act else 0, _stream_handle(device))
     _lib.check("sidon_gemm_bias_act", rc)
+    return out
+
+
+def linear_silu_lt(x: torch.Tensor, w: torch.Tensor, b: torch.Tensor | None, out: torch.Tensor | None = None,
+                   act: bool = True) -> torch.Tensor:
+    """silu(x . w^T + b) [M, N] fp16 on hipBLASLt with the bias and SiLU in
+    its epilogue (fp32 sum + bias, SiLU in fp32, one rounding to fp16), for
+    x [M, K] and w [N, K] fp16 (rows K-contiguous), b [N] fp16 or None;
+    act=False leaves out the SiLU.  The first call on a device must not run
+    during stream capture."""
+    device = x.device
+    rows, n, k, out = _linear_args(x, w, b, out)
+    lib = _lib.load()
+    with torch.cuda.device(device):
+        rc = lib.sidon_gemm_lt_act(x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0),
+                                   None if b is None else b.data_ptr(), out.data_ptr(), out.stride(0), rows, n, k,
+                                   1 if act else 0, _stream_handle(device))
+    _lib.check("sidon_gemm_lt_act", rc)
     return out
 
 

@@ -21,7 +21,7 @@ torch, the residual projections into the fp32 stream (one HIP kernel while
 its 64 x 64 tiles fit one per CU, else hipBLASLt), the pointwise conv's first
 GEMM on rocBLAS with the kernel chosen by timing (``blas.gemm_nt``), the
 feed-forward input projections with bias and SiLU (one HIP GEMM kernel where
-its tiles fill the chip, else hipBLASLt followed by the in-place HIP SiLU),
+its tiles fill the chip, else hipBLASLt with the bias and SiLU in its epilogue),
 the relative_key attention (HIP), and the conv module's GLU + causal
 depthwise conv + LayerNorm + SiLU as one HIP kernel reading the pointwise
 conv's output.  Every op launches on the current stream, reads no
@@ -37,7 +37,7 @@ from pathlib import Path
 import torch
 
 from .blas import gemm_nt
-from .conformer import (glu_causal_dw_norm, linear_silu, linear_silu_preferred, residual_gemm,
+from .conformer import (glu_causal_dw_norm, linear_silu, linear_silu_lt, linear_silu_preferred, residual_gemm,
                         residual_gemm_preferred, silu_)
 from .encoder_attention import flexrel_attention
 from .encoder_block import res_norm
@@ -157,11 +157,13 @@ class HipEncoder:
     """fp32 features [B, L, F] (+ valid frames [B]) -> hidden [B, L, C] fp32 on
     packed weights (``pack_encoder`` / ``pack_weights``)."""
 
-    def __init__(self, packed: dict, device="cuda", fused_ffn: bool | None = None,
+    def __init__(self, packed: dict, device="cuda", fused_ffn: bool | str | None = None,
                  own_residual: bool | None = None) -> None:
-        """fused_ffn: the feed-forward input projections as one GEMM + bias +
-        SiLU kernel (True), as hipBLASLt + SiLU (False), or chosen per call
-        by shape (None).  own_residual: the residual projections on this
+        """fused_ffn: the feed-forward input projections as this library's
+        GEMM + bias + SiLU kernel (True), as hipBLASLt with the bias and SiLU
+        in its epilogue ("lt"), as torch.addmm followed by a SiLU pass
+        (False), or chosen per call by shape (None: this library's kernel
+        where it is expected to be faster, else "lt").  own_residual: the residual projections on this
         library's kernel (True, ``conformer.residual_gemm``), on torch.addmm
         (False), or chosen per call by shape (None)."""
         device = torch.device(device)
@@ -229,9 +231,11 @@ class HipEncoder:
 
         fused = self.fused_ffn
         if fused is None:
-            fused = linear_silu_preferred(rows, self.inter, hid, device)
+            fused = True if linear_silu_preferred(rows, self.inter, hid, device) else "lt"
 
         def ffn_in(w, b):
+            if fused == "lt":
+                return linear_silu_lt(xn, w, b, out=h_buf)
             if fused:
                 return linear_silu(xn, w, b, out=h_buf)
             return silu_(torch.addmm(b, xn, w.t(), out=h_buf))

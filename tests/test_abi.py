@@ -186,6 +186,33 @@ def test_gemm_rejects_bad_arguments_before_launch(sidon, over, code):
     assert lib.sidon_last_error().decode()
 
 
+@pytest.mark.parametrize("over,code", [
+    (dict(x=None), -1),
+    (dict(w=None), -1),
+    (dict(y=None), -1),
+    (dict(M=0), -2),
+    (dict(N=0), -2),
+    (dict(K=0), -2),
+    (dict(act=2), -2),
+    (dict(M=1 << 20, ldx=4096, ldw=4096, K=4096), -2),  # 2^32 elements
+    (dict(ldx=1000), -3),
+    (dict(ldw=1000), -3),
+    (dict(ldy=4095), -3),
+    (dict(x=17), -4),
+    (dict(bias=13), -4),
+    (dict(y=33), -4),
+])
+def test_lt_gemm_rejects_bad_arguments_before_launch(sidon, over, code):
+    # fake addresses, never dereferenced: validation returns before any HIP call
+    lib = sidon._lib.load()
+    args = dict(x=16, ldx=1024, w=16, ldw=1024, bias=16, y=16, ldy=4096, M=750, N=4096, K=1024, act=1)
+    args.update(over)
+    rc = lib.sidon_gemm_lt_act(args["x"], args["ldx"], args["w"], args["ldw"], args["bias"], args["y"],
+                               args["ldy"], args["M"], args["N"], args["K"], args["act"], None)
+    assert rc == code
+    assert lib.sidon_last_error().decode()
+
+
 def test_residual_gemm_shape_support(sidon):
     lib = sidon._lib.load()
     assert lib.sidon_gemm_res_fits(750, 1024, 4096) == 1

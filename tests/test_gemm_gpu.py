@@ -1,6 +1,7 @@
-"""The fused feed-forward input projection (GEMM + bias + SiLU, csrc/gemm.hip)
-against float32 torch and against hipBLASLt followed by the in-place SiLU
-(needs an MI355X)."""
+"""The fused feed-forward input projection (GEMM + bias + SiLU, csrc/gemm.hip;
+hipBLASLt with the bias and SiLU in its epilogue, csrc/blaslt.hip) against
+float32 torch and against hipBLASLt followed by the in-place SiLU, and the
+residual GEMM (csrc/gemm_res.hip) (needs an MI355X)."""
 
 from __future__ import annotations
 
@@ -77,6 +78,85 @@ def test_linear_silu_out_buffer_and_strides(sidon):
     assert torch.allclose(out.float(), _reference(x, w, b, True).float(), atol=2e-3, rtol=2e-3)
 
 
+def _reference_lt(x, w, b, act):
+    """fp32 sums, bias added, SiLU in fp32, one rounding to fp16."""
+    h = x.float() @ w.float().t()
+    if b is not None:
+        h = h + b.float()
+    return (torch.nn.functional.silu(h) if act else h).half()
+
+
+@pytest.mark.parametrize("m,n,k,bias,act,ldx", [
+    (750, 4096, 1024, True, True, None),
+    (1500, 4096, 1024, True, True, None),
+    (333, 256, 64, False, False, None),
+    (1, 256, 128, True, True, None),
+    (650, 768, 128, True, True, 192),
+    (7, 96, 40, True, True, None),
+])
+def test_linear_silu_lt_matches_fp32(sidon, m, n, k, bias, act, ldx):
+    """hipBLASLt with the bias and SiLU in its epilogue against float32 torch,
+    and five more calls bit-identical to the first."""
+    x, w, b = _inputs(m, n, k, seed=m + n + k + 1, ldx=ldx)
+    b = b if bias else None
+    got = sidon.conformer.linear_silu_lt(x, w, b, act=act)
+    ref = _reference_lt(x, w, b, act)
+    torch.cuda.synchronize()
+    err = (got.float() - ref.float()).abs()
+    tol = 2e-3 + 2e-3 * ref.float().abs()
+    assert torch.isfinite(got.float()).all()
+    assert (err <= tol).all(), float(err.max())
+    snr = 10 * torch.log10(ref.float().pow(2).sum() / (got.float() - ref.float()).pow(2).sum().clamp_min(1e-30))
+    assert snr > 60, float(snr)
+    for _ in range(5):
+        again = sidon.conformer.linear_silu_lt(x, w, b, act=act)
+        assert torch.equal(again, got)
+
+
+def test_linear_silu_lt_out_buffer_and_strides(sidon):
+    """A strided output view: untouched columns stay untouched."""
+    x, w, b = _inputs(500, 256, 128, seed=12)
+    big = torch.full((500, 512), 5.0, dtype=torch.float16, device=DEV)
+    out = big[:, 128:384]
+    sidon.conformer.linear_silu_lt(x, w, b, out=out)
+    torch.cuda.synchronize()
+    assert torch.all(big[:, :128] == 5.0) and torch.all(big[:, 384:] == 5.0)
+    assert torch.allclose(out.float(), _reference_lt(x, w, b, True).float(), atol=2e-3, rtol=2e-3)
+
+
+def test_linear_silu_lt_agrees_with_fused_kernel(sidon):
+    """At the encoder's 15 s shape the epilogue SiLU (one rounding) and this
+    library's kernel (SiLU of the fp16-rounded sum) differ by at most about
+    one fp16 rounding step."""
+    x, w, b = _inputs(750, 4096, 1024, seed=17)
+    lt = sidon.conformer.linear_silu_lt(x, w, b)
+    own = sidon.conformer.linear_silu(x, w, b)
+    torch.cuda.synchronize()
+    diff = (lt.float() - own.float()).abs()
+    print(f"epilogue vs fused kernel: max {float(diff.max()):.3e}, differing {float((diff > 0).float().mean()):.4f}")
+    assert torch.allclose(lt.float(), own.float(), atol=2e-3, rtol=2e-3)
+
+
+def test_linear_silu_lt_graph_replays_match_eager(sidon):
+    """Captured into a HIP graph (after an eager call of the same problem) and
+    replayed three times, with eager work and synchronisations between the
+    replays: every replay equals the eager call."""
+    x, w, b = _inputs(1500, 4096, 1024, seed=19)
+    out = torch.empty(1500, 4096, dtype=torch.float16, device=DEV)
+    sidon.conformer.linear_silu_lt(x, w, b, out=out)
+    torch.cuda.synchronize()
+    eager = out.clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        sidon.conformer.linear_silu_lt(x, w, b, out=out)
+    for rep in range(3):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), rep
+        _ = (x.float() * 2).sum().item()  # unrelated eager work
+
+
 def test_encoder_fused_and_library_ffn_agree(sidon):
     """The whole encoder at Sidon's full width (8 layers, L=750) with the fused
     FFN input kernel forced on and forced off, and the fused one against the
@@ -92,14 +172,23 @@ def test_encoder_fused_and_library_ffn_agree(sidon):
     frames = torch.tensor([750], dtype=torch.int32, device=DEV)
     on = sidon.encoder.HipEncoder(packed, DEV, fused_ffn=True)(feats, frames)
     off = sidon.encoder.HipEncoder(packed, DEV, fused_ffn=False)(feats, frames)
+    lt = sidon.encoder.HipEncoder(packed, DEV, fused_ffn="lt")(feats, frames)
+    default = sidon.encoder.HipEncoder(packed, DEV)(feats, frames)
     torch.cuda.synchronize()
+    assert torch.equal(default, lt)  # at L = 750 the per-call choice is the epilogue path
     agree = errors(off[0].double().cpu().numpy(), on[0].double().cpu().numpy())
     want = encoder_reference(feats, weights, [750], dtype=torch.float32)
     err = errors(want[0].double().cpu().numpy(), on[0].double().cpu().numpy())
-    print("fused vs library FFN input:", agree, "fused vs fp32 oracle:", err)
-    assert torch.isfinite(on).all()
+    # The epilogue path rounds the SiLU input differently (no fp16 rounding of
+    # the biased sum), so it is held to the oracle, not to the other paths.
+    err_lt = errors(want[0].double().cpu().numpy(), lt[0].double().cpu().numpy())
+    err_off = errors(want[0].double().cpu().numpy(), off[0].double().cpu().numpy())
+    print("fused vs library FFN input:", agree, "vs fp32 oracle: fused", err, "epilogue", err_lt, "addmm + SiLU",
+          err_off)
+    assert torch.isfinite(on).all() and torch.isfinite(lt).all()
     assert agree["snr_db"] > 80, agree
     assert err["snr_db"] > 58 and err["max_abs"] < 0.02 * want.abs().max().item(), err
+    assert err_lt["snr_db"] > 58 and err_lt["max_abs"] < 0.02 * want.abs().max().item(), err_lt
 
 
 def test_linear_silu_graph_replays_match_eager(sidon):
