@@ -41,9 +41,14 @@ PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
 B, H, L, D, LAYERS = 1, 16, 4800, 64, 8
 COPY_PROBE_BYTES = 256 << 20  # --copy-probe: one device copy of this many bytes
 XCDS = 8  # MI355X: GRBM_GUI_ACTIVE is summed over the 8 accelerator complex dies
+SIMDS = 1024  # 256 compute units x 4 SIMDs
+MFMA_FLOPS_PER_SIMD_CYCLE = 1024.0  # dense fp16: 2.5 PFLOP/s = 1024 SIMDs x 1024 flop x 2.4 GHz
 # Algorithmic HBM bytes of one c3 launch: q, k and v read once, the output
 # written once, the 73x64 table and the valid length.
 ALGO_BYTES = 3 * B * L * H * D * 2 + B * L * H * D * 2 + 73 * D * 2 + 4 * B
+
+
+FLOPS_LAUNCH = 1.0 * B * H * (4.0 * L * L * D + 2.0 * L * 73 * D)  # one c3 attention launch
 
 
 def log(*a):
@@ -103,6 +108,29 @@ def c3_workload(torch, sidon, dev):
             "lens": lens, "attn": attn, "graphs": graphs, "graph": graph}
 
 
+SETTLE_MS = [300.0]  # set from --settle-ms
+
+
+def settle_clock(torch, graph) -> dict:
+    """Replays ``graph`` back to back until SETTLE_MS of wall time have passed
+    (at least 20 replays), before the warm-up replays: a fresh process's
+    first ~80 attention launches run 5-20% slower while the GPU clock rises
+    from idle, so without this a short warm-up leaves the ramp inside the
+    timed pass.  Untimed; the count is reported."""
+    budget = SETTLE_MS[0] / 1e3
+    if budget <= 0:
+        return {"replays": 0, "ms": 0.0}
+    n, t0 = 0, time.perf_counter()
+    while True:
+        for _ in range(20):
+            graph.replay()
+        n += 20
+        torch.cuda.synchronize()
+        if time.perf_counter() - t0 >= budget:
+            break
+    return {"replays": n, "ms": (time.perf_counter() - t0) * 1e3}
+
+
 def host_cpu() -> dict:
     """This host's CPU: model and sockets from lscpu, os.cpu_count() and the
     cores this process may run on (its affinity set)."""
@@ -135,7 +163,7 @@ def _median_s(fn, runs, warmup=1):
     return statistics.median(samples)
 
 
-def cpu_baseline(torch, qkv_host, rels) -> dict:
+def cpu_baseline(torch, qkv_host, rels, gpu_outs=None) -> dict:
     """The reference's CPU fp32 path (oracle.torch_core_chunked, the fp32
     torch restatement of flexrel_triton.py:297-328, 512-row chunks) timed on
     this host with one thread per core of the affinity set:
@@ -145,8 +173,13 @@ def cpu_baseline(torch, qkv_host, rels) -> dict:
       * c1: one call at L=750 on fp32 q/k/v ~N(0,1)/8, median of 5;
       * c2: one call at L=1500 with 1463 valid keys (fp16 inputs upcast),
         median of 3.
+    With ``gpu_outs`` (the benched layers' fp16 outputs [L, H*64], on the
+    host), the fp32 outputs of the timed chunk are also the checker of the
+    benched graph: per layer max_abs and SNR (oracle.errors, the metric of
+    engines.py:47-55) over every row, against the north star's bar
+    (SNR >= 60 dB, max_abs <= 2e-3).
     """
-    from oracle.flexrel_oracle import torch_core_chunked
+    from oracle.flexrel_oracle import errors, torch_core_chunked
 
     host = host_cpu()
     threads = host["affinity"]
@@ -156,12 +189,26 @@ def cpu_baseline(torch, qkv_host, rels) -> dict:
         view = qkv.view(B, L, 3, H, D)
         q, k, v = (view[:, :, i].permute(0, 2, 1, 3).float().contiguous() for i in range(3))
         layers.append((q, k, v, rel.float()))
+    outs_cpu = [torch.empty(B, H, L, D) for _ in layers]
 
     def chunk():
-        for q, k, v, rel in layers:
-            torch_core_chunked(q, k, v, rel)
+        for (q, k, v, rel), o in zip(layers, outs_cpu):
+            torch_core_chunked(q, k, v, rel, out=o)
     torch_core_chunked(*layers[0])  # warm-up: one layer
     c3_s = _median_s(chunk, 3, warmup=0)
+    parity = None
+    if gpu_outs is not None:
+        per = []
+        for o_cpu, o_gpu in zip(outs_cpu, gpu_outs):
+            got = o_gpu.view(B, L, H, D).permute(0, 2, 1, 3).float()
+            e = errors(o_cpu.numpy(), got.numpy())
+            per.append({"snr_db": e["snr_db"], "max_abs": e["max_abs"]})
+        parity = {"reference": "fp32 torch relative_key attention (oracle.torch_core_chunked) on each layer's "
+                               "own fp16 q/k/v, all rows; errors as engines.py:47-55",
+                  "min_snr_db": min(x["snr_db"] for x in per), "max_abs": max(x["max_abs"] for x in per),
+                  "bar": {"snr_db": 60.0, "max_abs": 2e-3},
+                  "pass": all(x["snr_db"] >= 60.0 and x["max_abs"] <= 2e-3 for x in per),
+                  "per_layer": per}
 
     gen = torch.Generator().manual_seed(101)
     c1 = [torch.randn(1, H, 750, D, generator=gen) / 8 for _ in range(3)]
@@ -182,6 +229,7 @@ def cpu_baseline(torch, qkv_host, rels) -> dict:
         "c1_ms_per_call": c1_s * 1e3,
         "c2_ms_per_call": c2_s * 1e3,
         "host": host,
+        "parity": parity,
     }
 
 
@@ -583,9 +631,10 @@ def _pmc_pass(prof: str, counters: list, probe: str, out: Path) -> tuple:
 
 
 def measure_counters() -> dict:
-    """HBM traffic and clock of the attention kernel on the c3 shape,
-    measured in this run: four rocprofv3 counter passes over child
-    processes (FETCH_SIZE with GRBM_GUI_ACTIVE, then WRITE_SIZE, on
+    """HBM traffic, clock and matrix-core occupancy of the attention kernel
+    on the c3 shape, measured in this run: four rocprofv3 counter passes over
+    child processes (FETCH_SIZE with GRBM_GUI_ACTIVE, then WRITE_SIZE with
+    GRBM_GUI_ACTIVE, SQ_VALU_MFMA_BUSY_CYCLES and SQ_BUSY_CYCLES, on
     `--kernel-probe`: three launches of layer 0; the same two on
     `--copy-probe`: device copies of 256 MiB, whose counter readings per
     byte calibrate the KiB the counters report).  Runs before this process
@@ -600,7 +649,8 @@ def measure_counters() -> dict:
         tmp = Path(tmp)
         per = {}
         for key, counters, probe in (("kernel_fetch", ["FETCH_SIZE", "GRBM_GUI_ACTIVE"], "--kernel-probe"),
-                                     ("kernel_write", ["WRITE_SIZE"], "--kernel-probe"),
+                                     ("kernel_write", ["WRITE_SIZE", "GRBM_GUI_ACTIVE", "SQ_VALU_MFMA_BUSY_CYCLES",
+                                                       "SQ_BUSY_CYCLES"], "--kernel-probe"),
                                      ("copy_fetch", ["FETCH_SIZE"], "--copy-probe"),
                                      ("copy_write", ["WRITE_SIZE"], "--copy-probe")):
             log(f"counters: {key} ({' '.join(counters)}) ...")
@@ -634,6 +684,21 @@ def summarize_counters(per: dict) -> dict:
     dur_ns = med(dur[d] for d in ds if d in dur) if any(d in dur for d in ds) else None
     ds_w, vals_w, _ = pick("kernel_write", "flexrel")
     write_kib = med(vals_w[d]["WRITE_SIZE"] for d in ds_w)
+    # Matrix-core occupancy: SQ_VALU_MFMA_BUSY_CYCLES is summed over every
+    # SIMD of the chip, so dividing by the launch's cycles (GRBM_GUI_ACTIVE of
+    # the same pass / 8 XCDs) and by the SIMD count gives the busy fraction.
+    mfma = {}
+    if all("SQ_VALU_MFMA_BUSY_CYCLES" in vals_w[d] and "GRBM_GUI_ACTIVE" in vals_w[d] for d in ds_w):
+        cyc = med(vals_w[d]["GRBM_GUI_ACTIVE"] for d in ds_w) / XCDS
+        busy = med(vals_w[d]["SQ_VALU_MFMA_BUSY_CYCLES"] for d in ds_w)
+        useful = FLOPS_LAUNCH / MFMA_FLOPS_PER_SIMD_CYCLE
+        mfma = {"sq_valu_mfma_busy_cycles": busy, "sq_busy_cycles": med(vals_w[d].get("SQ_BUSY_CYCLES", 0.0) for d in ds_w),
+                "cycles_per_launch": cyc, "mfma_busy_frac": busy / cyc / SIMDS,
+                "mfma_useful_frac": useful / cyc / SIMDS,
+                "mfma_note": "mfma_busy_frac = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / 8) / 1024 SIMDs (row-sum "
+                             "and q.rel products included); mfma_useful_frac = the launch's algorithmic flops / "
+                             "(1024 flop per SIMD-cycle x 1024 SIMDs x cycles), i.e. TFLOP/s against the peak at "
+                             "the clock the launch ran at"}
     cds, cvals, _ = pick("copy_fetch", "opy")
     copy_fetch_kib = med(cvals[d]["FETCH_SIZE"] for d in cds)
     cds_w, cvals_w, _ = pick("copy_write", "opy")
@@ -647,6 +712,7 @@ def summarize_counters(per: dict) -> dict:
                 "traffic_over_algorithmic": traffic / ALGO_BYTES, "grbm_gui_active": grbm,
                 "kernel_ns_under_counters": dur_ns,
                 "sclk_mhz": (grbm / XCDS / dur_ns * 1e3) if dur_ns else None})
+    res.update(mfma)
     return res
 
 
@@ -689,7 +755,12 @@ def main() -> int:
     ap.add_argument("--enc-lengths", default=",".join(str(x) for x in ENC_LENGTHS),
                     help="--workload encoder: comma-separated chunk lengths (frames) to time, last = headline")
     ap.add_argument("--no-counters", action="store_true",
-                    help="skip the rocprofv3 counter passes (HBM traffic and clock of the c3 kernel)")
+                    help="skip the rocprofv3 counter passes (HBM traffic, clock and MFMA busy of the c3 kernel)")
+    ap.add_argument("--no-extra-workloads", action="store_true",
+                    help="c3: skip timing the c4 sweep and the c5 sub-block as extra keys of the line")
+    ap.add_argument("--settle-ms", type=float, default=300.0,
+                    help="c3: replay the graph for this long before the warm-up replays, so the timed pass does "
+                         "not include the clock's ramp from idle (0 disables)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py runs on one GPU only: this build has no multi-GPU path "
@@ -697,6 +768,7 @@ def main() -> int:
               "chunks, with no collectives)", file=sys.stderr)
         return 2
 
+    SETTLE_MS[0] = args.settle_ms
     if args.kernel_probe:
         return kernel_probe()
     counters = None
@@ -748,6 +820,7 @@ def main() -> int:
     h0, rels, projs_d, qkv, outs, lens = w["h0"], w["rels"], w["projs_d"], w["qkv"], w["outs"], w["lens"]
     rels_d, attn, graphs, graph = w["rels_d"], w["attn"], w["graphs"], w["graph"]
     stream = torch.cuda.current_stream()
+    settle = settle_clock(torch, graph)
     for _ in range(args.warmup):
         graph.replay()
     torch.cuda.synchronize()
@@ -776,8 +849,11 @@ def main() -> int:
     achieved = flops_launch / (launch_us * 1e-6) / 1e12
 
     extra = {"median_ms": statistics.median(per_step), "min_ms": min(per_step),
-             "kernel_avg_us": launch_us, "tflops": achieved,
-             "pct_fp16_peak": 100.0 * achieved / PEAK_TFLOPS, "launch": shape}
+             "launch_avg_us": launch_us,
+             "launch_avg_note": "ms_per_step / 8: HIP events on the graph's stream around the K timed replays of "
+                                "8 back-to-back launches (the roofline's launch time)",
+             "tflops": achieved, "pct_fp16_peak": 100.0 * achieved / PEAK_TFLOPS, "launch": shape,
+             "clock_settle": settle}
 
     if not args.no_projections:
         # Secondary: the same 8 layers with the residual update and the next
@@ -806,6 +882,19 @@ def main() -> int:
         extra["with_projections_ms"] = c0.elapsed_time(c1) / 10
 
     extra["gpu_per_call_us"] = gpu_per_call(torch, sidon, dev)
+    gpu_outs = [o.cpu() for o in outs]  # the timed graph's outputs (every replay writes the same)
+
+    if not args.no_extra_workloads:
+        # The other BASELINE configs timed in the same run (untimed for `value`): the c4 bucket sweep
+        # and the c5 sub-block; each builds and releases its own state.
+        c4 = run_c4(torch, sidon, args)
+        extra["c4"] = {"ms": c4["value"], "tflops_aggregate": c4["tflops_aggregate"], "buckets": c4["config"]["buckets"],
+                       "workload": c4["config"]["workload"]}
+        del c4
+        c5 = run_c5(torch, sidon, args)
+        extra["c5"] = {"ms": c5["value"], "tflops": c5["tflops"], "workload": c5["config"]["workload"]}
+        del c5
+        torch.cuda.synchronize()
 
     traffic = counters.get("traffic_bytes") if counters else None
     extra["counters"] = counters
@@ -832,7 +921,8 @@ def main() -> int:
     result.update(extra)
     if not args.no_cpu_baseline:
         log("timing the CPU baseline ...")
-        result["cpu_baseline"] = cpu_baseline(torch, [t.cpu() for t in qkv], rels)
+        result["cpu_baseline"] = cpu_baseline(torch, [t.cpu() for t in qkv], rels, gpu_outs)
+        result["parity"] = result["cpu_baseline"].pop("parity")
     print(json.dumps(result), flush=True)
     return 0
 

@@ -105,7 +105,8 @@ int sidon_gemm_lt_act(const void* x, int ldx, const void* w, int ldw, const void
  * over the workgroup's 4 wavefronts and summed in a fixed order: the result
  * does not depend on timing.  Shapes: M >= 1, N a multiple of 64, K a
  * multiple of 128; ldx, ldw multiples of 8 and >= K, ldy a multiple of 4 and
- * >= N; x, w, y 16-byte aligned; x and w must not overlap y.  sidon_gemm_res_fits(M, N, K) says whether
+ * >= N; x, w, y 16-byte aligned; x and w must not overlap y (checked on the byte ranges
+ * the call touches: SIDON_E_SHAPE).  sidon_gemm_res_fits(M, N, K) says whether
  * a shape is supported (pure host function); sidon_gemm_res_preferred(M, N,
  * K) whether the kernel is expected to beat a library GEMM on the current
  * device (its tiles fit one per compute unit).  Neither has a counterpart in
@@ -141,7 +142,10 @@ int sidon_gemm_res(const void* x, int ldx, const void* w, int ldw, float* y, int
  * the problem's beta from identical contents; fp32 output: every row and
  * column within 1e-5 relative; fp16 output: every element within one fp16
  * ulp and the whole within 1e-4 -- and writes its solution index to
- * *solution_out (INT_MIN: the default) when that is not NULL.  The tuner
+ * *solution_out (INT_MIN: the default) when that is not NULL.  When no
+ * listed kernel is free of workspace or none passes that gate, it records
+ * rocBLAS's default and returns SIDON_OK (SIDON_GEMM_TUNE_FORCE_FALLBACK=1
+ * takes that path for every problem, for tests).  The tuner
  * synchronises the stream and fails during stream capture; tune before
  * capturing.  Every candidate is deterministic (rocBLAS atomics disabled),
  * but the choice is by timing, so two processes may keep different kernels
@@ -239,7 +243,10 @@ int sidon_fbank_normalize(const float* logmel, const int* valid, float* workspac
  * items (any F); larger B returns SIDON_E_SHAPE.  Every call on one device
  * shares that device's array, so calls that overlap on one GPU (two streams,
  * two threads) race; every word a call reads is written earlier in the same
- * call, so consecutive calls need no clearing.
+ * call, so consecutive calls need no clearing.  The first call on a device
+ * looks up the array's device address (hipGetSymbolAddress, once per device)
+ * and must run outside stream capture; later calls launch three kernels and
+ * nothing else (no memset, no copy), so they may be captured into a graph.
  */
 int sidon_fbank_normalize_noalloc(const float* logmel, const int* valid, float* feats, int B, int F,
                                   sidon_stream_t stream);

@@ -54,6 +54,7 @@ typedef struct ihipStream_t* sidon_stream_t;
 #define SIDON_E_ALIGN (-4)     /* base pointer not 16-byte aligned */
 #define SIDON_E_LAUNCH (-5)    /* the HIP launch itself failed */
 #define SIDON_E_DEVICE (-6)    /* no usable HIP device / wrong architecture */
+#define SIDON_E_CONFIG (-7)    /* SIDON_FLEXREL_VARIANT names no kernel (split8, w64, w32, auto) */
 
 /*
  * Strided [B, H, L, 64] attention.
@@ -90,10 +91,15 @@ int sidon_flexrel_fwd_qkv(const void* qkv, const void* rel,
 
 /*
  * Launch shape chosen for a given (B, H, L): queries per workgroup and the
- * number of key splits merged inside a workgroup.  Pure host function (no
- * device access); exposed so tests and benchmarks can report it.  Has no
- * counterpart in the reference (Triton picks BLOCK_M/BLOCK_N at
- * src/sidon_triton/triton_encoder.py:340-343).
+ * number of key splits merged inside a workgroup.  Host function: it
+ * launches nothing and reads the current device's compute-unit count once
+ * (hipGetDeviceProperties); exposed so tests and benchmarks can report it.
+ * It reports the shape of calls whose K and V rows share one row stride
+ * (the fused QKV layout of sidon_flexrel_fwd_qkv); sidon_flexrel_fwd with K
+ * and V rows of different strides launches 64 rows x 8 key splits (512
+ * threads) instead.  Returns SIDON_E_CONFIG when SIDON_FLEXREL_VARIANT holds
+ * an unknown value.  Has no counterpart in the reference (Triton picks
+ * BLOCK_M/BLOCK_N at src/sidon_triton/triton_encoder.py:340-343).
  */
 int sidon_flexrel_launch_shape(int B, int H, int L, int* queries_per_block,
                                int* key_splits, int* workgroups,

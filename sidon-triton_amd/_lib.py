@@ -20,6 +20,7 @@ ERROR_NAMES = {
     -4: "SIDON_E_ALIGN",
     -5: "SIDON_E_LAUNCH",
     -6: "SIDON_E_DEVICE",
+    -7: "SIDON_E_CONFIG",
 }
 
 # Every symbol include/*.h declares, with its ctypes signature.

@@ -18,7 +18,7 @@ PKG_DIR = Path(__file__).resolve().parent
 REPO_DIR = PKG_DIR.parent
 LIB_NAME = "libsidon_flexrel.so"
 SOURCES = [PKG_DIR / "csrc" / name
-           for name in ("flexrel_fwd.hip", "flexrel_wide.hip", "flexrel_w64.hip", "flexrel_w32.hip", "res_norm.hip", "conformer_ops.hip", "fbank.hip", "gemm.hip", "gemm_res.hip", "blas.hip", "blaslt.hip")]
+           for name in ("flexrel_fwd.hip", "flexrel_w64.hip", "flexrel_w32.hip", "res_norm.hip", "conformer_ops.hip", "fbank.hip", "gemm.hip", "gemm_res.hip", "blas.hip", "blaslt.hip")]
 # rocBLAS for the plain GEMMs of csrc/blas.hip.  Its soname is the one torch
 # bundles, so inside a torch process the library shares torch's copy.
 LIBS = ["-lrocblas", "-lhipblaslt"]
@@ -48,10 +48,10 @@ def hipcc() -> str:
 
 
 def generate(verbose: bool = False) -> None:
-    """Writes csrc/flexrel_wide_step.inc (the hand-scheduled key-step loop of
-    flexrel_wide.hip) from csrc/gen_wide_step.py, which also checks its wait
+    """Writes csrc/flexrel_w64_step.inc (the hand-scheduled key-step loop of
+    flexrel_w64.hip) from csrc/gen_w64_step.py, which also checks its wait
     states and load accounting."""
-    for name in ("gen_wide_step.py", "gen_w64_step.py"):
+    for name in ("gen_w64_step.py",):
         gen = PKG_DIR / "csrc" / name
         proc = subprocess.run([sys.executable, str(gen)], capture_output=True, text=True)
         if proc.returncode != 0:

@@ -1,7 +1,6 @@
 // flexrel_device.h -- device helpers and launch parameters shared by the
 // relative_key attention kernels (flexrel_fwd.hip: 64 query rows per
-// workgroup, 8 key splits; flexrel_wide.hip: 128 query rows per wavefront,
-// 4 key splits; flexrel_w64.hip: 64 rows per wavefront, 4 key splits, two
+// workgroup, 8 key splits; flexrel_w64.hip: 64 rows per wavefront, 4 key splits, two
 // workgroups per compute unit; flexrel_w32.hip: 32 rows per wavefront, 4 key
 // splits, for short sequences).  Internal to the library.
 #pragma once
@@ -189,12 +188,7 @@ __device__ __forceinline__ int fresh_lane_id() {
 
 }  // namespace sidon_flexrel
 
-// Launch of the 128-row kernel (flexrel_wide.hip) for workgroups
-// [0, nwg) of p, with p.nqb = query blocks of 128 rows per (b, h).
 namespace sidon_flexrel {
-int wide_rows();
-int wide_threads();
-hipError_t launch_wide(const Params& p, int nwg, bool same_stride, hipStream_t stream);
 // Launch of the 64-row, two-workgroups-per-CU kernel (flexrel_w64.hip), with
 // p.nqb = query blocks of 64 rows per (b, h).
 int w64_rows();

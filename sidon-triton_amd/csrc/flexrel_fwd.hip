@@ -704,10 +704,11 @@ int g_dev_status[kMaxDevices];
 int g_dev_cus[kMaxDevices];
 }  // namespace
 
-int check_device() {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return fail(SIDON_E_DEVICE, "hipGetDevice failed");
-  if (dev < 0 || dev >= kMaxDevices) return fail(SIDON_E_DEVICE, "device index %d out of range", dev);
+// The one-time query of device dev: 1 (gfx950), -1 (query failed), -2 (other
+// architecture).  g_dev_status / g_dev_cus are written only inside the
+// call_once and read only after it returned, which orders every read after
+// the write on any thread.
+int device_status(int dev) {
   std::call_once(g_dev_flags[dev], [dev]() {
     hipDeviceProp_t prop;
     if (hipGetDeviceProperties(&prop, dev) != hipSuccess) {
@@ -717,14 +718,24 @@ int check_device() {
     g_dev_cus[dev] = prop.multiProcessorCount;
     g_dev_status[dev] = strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : -2;
   });
-  if (g_dev_status[dev] == -1) return fail(SIDON_E_DEVICE, "hipGetDeviceProperties failed on device %d", dev);
-  if (g_dev_status[dev] != 1) return fail(SIDON_E_DEVICE, "device %d is not gfx950", dev);
+  return g_dev_status[dev];
+}
+
+int check_device() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(SIDON_E_DEVICE, "hipGetDevice failed");
+  if (dev < 0 || dev >= kMaxDevices) return fail(SIDON_E_DEVICE, "device index %d out of range", dev);
+  const int st = device_status(dev);
+  if (st == -1) return fail(SIDON_E_DEVICE, "hipGetDeviceProperties failed on device %d", dev);
+  if (st != 1) return fail(SIDON_E_DEVICE, "device %d is not gfx950", dev);
   return SIDON_OK;
 }
 
+// Compute units of the current device (MI355X: 256); 256 when no gfx950
+// device can be queried (host-only shape queries).
 int compute_units() {
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices || g_dev_status[dev] != 1) return 256;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices || device_status(dev) != 1) return 256;
   return g_dev_cus[dev];
 }
 
@@ -735,24 +746,23 @@ namespace {
 // Kernel variants: the 64-row workgroup with 8 key splits and one workgroup
 // per compute unit (flexrel_fwd_kernel, any K / V strides); the 64-row
 // workgroup with 4 key splits and two workgroups per compute unit
-// (flexrel_w64.hip); the 128-row wavefront with 4 key splits (flexrel_wide.hip)
-// over all rows; and the wide kernel over as many 128-row blocks as fill
-// whole rounds of the chip, the remaining rows then running on the 8-split
-// kernel in a second launch; the 32-row workgroup with 4 key splits
+// (flexrel_w64.hip); the 32-row workgroup with 4 key splits
 // (flexrel_w32.hip) for short sequences.
-enum Variant { kSplit8 = 0, kWide = 1, kWideTail = 2, kW64 = 3, kW32 = 4 };
+enum Variant { kSplit8 = 0, kW64 = 3, kW32 = 4 };
 
-// SIDON_FLEXREL_VARIANT=split8|wide|wide_tail|w64|w32 forces one variant (A/B
-// timing and tests; read at every call); unset or "auto" picks by shape.
+// SIDON_FLEXREL_VARIANT=split8|w64|w32 forces one variant (A/B timing and
+// tests); unset, empty or "auto" picks by shape; any other value is an error
+// (SIDON_E_CONFIG), so a mistyped override never runs silently on the
+// automatic choice.  Read at every call that plans a launch (tests switch it
+// between calls); a graph captured under one setting keeps that launch.
+constexpr int kAuto = -1, kBadVariant = -2;
 int forced_variant() {
   const char* e = getenv("SIDON_FLEXREL_VARIANT");
-  if (e == nullptr) return -1;
+  if (e == nullptr || e[0] == '\0' || strcmp(e, "auto") == 0) return kAuto;
   if (strcmp(e, "split8") == 0) return (int)kSplit8;
-  if (strcmp(e, "wide") == 0) return (int)kWide;
-  if (strcmp(e, "wide_tail") == 0) return (int)kWideTail;
   if (strcmp(e, "w64") == 0) return (int)kW64;
   if (strcmp(e, "w32") == 0) return (int)kW32;
-  return -1;
+  return kBadVariant;
 }
 
 // Automatic choice, from launch timings on MI355X (B = 1; H = 16 at
@@ -768,22 +778,31 @@ int forced_variant() {
 // Otherwise the two-workgroups-per-CU 64-row kernel is the fastest or level
 // with the fastest at every length (its key-step loop keeps the matrix core
 // busy with two wavefronts per SIMD; the 32-row kernel's pairs contend in
-// their latency-bound phases, the 8-split kernel's steps cost more, the
-// 128-row kernel's blocks are too few below a full round of the chip).  K
-// and V rows of different strides take the 8-split kernel.
+// their latency-bound phases, the 8-split kernel's steps cost more).  K and
+// V rows of different strides take the 8-split kernel, whatever the override.
 constexpr int kW32MaxKeys = 1024;
-Variant choose_variant(int B, int H, int L, bool same_stride) {
-  if (!same_stride) return kSplit8;  // the other kernels are built for K and V rows of one stride
+int choose_variant(int B, int H, int L, bool same_stride, Variant* out) {
+  if (!same_stride) {  // the other kernels are built for K and V rows of one stride
+    *out = kSplit8;
+    return SIDON_OK;
+  }
   const int f = forced_variant();
-  if (f >= 0) return (Variant)f;
+  if (f == kBadVariant)
+    return fail(SIDON_E_CONFIG, "SIDON_FLEXREL_VARIANT=%s is not one of split8, w64, w32, auto",
+                getenv("SIDON_FLEXREL_VARIANT"));
+  if (f != kAuto) {
+    *out = (Variant)f;
+    return SIDON_OK;
+  }
   const long long w32_blocks = (long long)B * H * ((L + w32_rows() - 1) / w32_rows());
-  return L <= kW32MaxKeys && w32_blocks <= sidon::compute_units() ? kW32 : kW64;
+  *out = L <= kW32MaxKeys && w32_blocks <= sidon::compute_units() ? kW32 : kW64;
+  return SIDON_OK;
 }
 
 // One launch: `rows` query rows per workgroup, nqb blocks per (b, h) from
 // query row row0.
 struct Launch {
-  Variant kernel;  // kSplit8, kWide, kW64 or kW32
+  Variant kernel;  // kSplit8, kW64 or kW32
   int rows, splits, threads, nqb, row0;
   long long nwg;
 };
@@ -795,60 +814,49 @@ struct Plan {
 Launch launch_of(Variant kernel, int B, int H, int nqb, int row0) {
   Launch x;
   x.kernel = kernel;
-  x.rows = kernel == kWide ? wide_rows() : kernel == kW64 ? w64_rows() : kernel == kW32 ? w32_rows() : kRows;
+  x.rows = kernel == kW64 ? w64_rows() : kernel == kW32 ? w32_rows() : kRows;
   x.splits = kernel == kSplit8 ? kWaves : 4;
-  x.threads = kernel == kWide  ? wide_threads()
-              : kernel == kW64 ? w64_threads()
-              : kernel == kW32 ? w32_threads()
-                               : kThreads;
+  x.threads = kernel == kW64 ? w64_threads() : kernel == kW32 ? w32_threads() : kThreads;
   x.nqb = nqb;
   x.row0 = row0;
   x.nwg = (long long)B * H * nqb;
   return x;
 }
 
-Plan plan_of(int B, int H, int L, bool same_stride = true) {
-  Plan pl;
-  const Variant v = choose_variant(B, H, L, same_stride);
-  pl.n = 1;
-  if (v == kWideTail) {
-    const int wr = wide_rows();
-    const long long cus = sidon::compute_units();
-    const long long rounds = (long long)B * H * (L / wr) / cus;  // whole rounds of 128-row blocks
-    const int nb = (int)(rounds * cus / ((long long)B * H));      // 128-row blocks per (b, h)
-    if (nb > 0) {
-      pl.l[0] = launch_of(kWide, B, H, nb, 0);
-      const int rest = L - nb * wr;
-      if (rest > 0) {
-        pl.l[1] = launch_of(kSplit8, B, H, (rest + kRows - 1) / kRows, nb * wr);
-        pl.n = 2;
-      }
-      return pl;
-    }
-    pl.l[0] = launch_of(kSplit8, B, H, (L + kRows - 1) / kRows, 0);
-    return pl;
-  }
-  if (v == kWide) {
-    pl.l[0] = launch_of(kWide, B, H, (L + wide_rows() - 1) / wide_rows(), 0);
-  } else if (v == kW64) {
-    pl.l[0] = launch_of(kW64, B, H, (L + w64_rows() - 1) / w64_rows(), 0);
-  } else if (v == kW32) {
-    pl.l[0] = launch_of(kW32, B, H, (L + w32_rows() - 1) / w32_rows(), 0);
-  } else {
-    pl.l[0] = launch_of(kSplit8, B, H, (L + kRows - 1) / kRows, 0);
-  }
-  return pl;
+int plan_of(int B, int H, int L, bool same_stride, Plan* pl) {
+  Variant v;
+  const int rc = choose_variant(B, H, L, same_stride, &v);
+  if (rc) return rc;
+  const int rows = v == kW64 ? w64_rows() : v == kW32 ? w32_rows() : kRows;
+  pl->n = 1;
+  pl->l[0] = launch_of(v, B, H, (L + rows - 1) / rows, 0);
+  return SIDON_OK;
 }
 
 }  // namespace
 
+namespace {
+// The plan of a call whose K and V rows have the same stride or not, with
+// the grid-size check of every launch.
+int checked_plan(int B, int H, int L, bool same_stride, Plan* pl) {
+  if (B < 1 || H < 1 || L < 1) return fail(SIDON_E_SHAPE, "B=%d H=%d L=%d must be >= 1", B, H, L);
+  const int rc = plan_of(B, H, L, same_stride, pl);
+  if (rc) return rc;
+  long long total = 0;
+  for (int i = 0; i < pl->n; ++i) total += pl->l[i].nwg;
+  if (total >= (1LL << 31)) return fail(SIDON_E_SHAPE, "grid of %lld workgroups too large", total);
+  return SIDON_OK;
+}
+}  // namespace
+
 SIDON_API int sidon_flexrel_launch_shape(int B, int H, int L, int* queries_per_block,
                                          int* key_splits, int* workgroups, int* threads_per_block) {
-  if (B < 1 || H < 1 || L < 1) return fail(SIDON_E_SHAPE, "B=%d H=%d L=%d must be >= 1", B, H, L);
-  const Plan pl = plan_of(B, H, L);
+  sidon::clear_error();
+  Plan pl;
+  const int rc = checked_plan(B, H, L, true, &pl);
+  if (rc) return rc;
   long long total = 0;
   for (int i = 0; i < pl.n; ++i) total += pl.l[i].nwg;
-  if (total >= (1LL << 31)) return fail(SIDON_E_SHAPE, "grid of %lld workgroups too large", total);
   // The first launch's shape; workgroups counts every launch of the call.
   if (queries_per_block) *queries_per_block = pl.l[0].rows;
   if (key_splits) *key_splits = pl.l[0].splits;
@@ -872,8 +880,10 @@ SIDON_API int sidon_flexrel_fwd(const void* q, const void* k, const void* v, con
     return rc;
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(rel) || !aligned16(out))
     return fail(SIDON_E_ALIGN, "q, k, v, rel and out must be 16-byte aligned");
-  if ((rc = sidon_flexrel_launch_shape(B, H, L, nullptr, nullptr, nullptr, nullptr))) return rc;
+  // the device first: the plan reads its compute-unit count
   if ((rc = check_device())) return rc;
+  Plan pl;
+  if ((rc = checked_plan(B, H, L, k_strides[2] == v_strides[2], &pl))) return rc;
 
   Params p;
   p.q = static_cast<const _Float16*>(q);
@@ -900,15 +910,12 @@ SIDON_API int sidon_flexrel_fwd(const void* q, const void* k, const void* v, con
   p.scale = 1.4426950408889634f / 8.0f;  // log2(e) / sqrt(64)
 
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const Plan pl = plan_of(B, H, L, p.ksl == p.vsl);
   hipError_t err = hipSuccess;
   for (int i = 0; i < pl.n && err == hipSuccess; ++i) {
     const Launch& x = pl.l[i];
     p.nqb = x.nqb;
     p.row0 = x.row0;
-    if (x.kernel == kWide) {
-      err = launch_wide(p, (int)x.nwg, true, s);
-    } else if (x.kernel == kW64) {
+    if (x.kernel == kW64) {
       err = launch_w64(p, (int)x.nwg, true, s);
     } else if (x.kernel == kW32) {
       err = launch_w32(p, (int)x.nwg, true, s);

@@ -316,6 +316,17 @@ SIDON_API int sidon_gemm_res(const void* x, int ldx, const void* w, int ldw, flo
     return fail(SIDON_E_SHAPE, "X and W must each span less than 4 GiB");
   if (!sidon::aligned16(x) || !sidon::aligned16(w) || !sidon::aligned16(y))
     return fail(SIDON_E_ALIGN, "x, w and y must be 16-byte aligned");
+  // Workgroups read X and W while others already add into Y: the byte
+  // ranges the call touches must be disjoint.
+  {
+    const uintptr_t xb = reinterpret_cast<uintptr_t>(x), wb = reinterpret_cast<uintptr_t>(w);
+    const uintptr_t yb = reinterpret_cast<uintptr_t>(y);
+    const uintptr_t xe = xb + (uintptr_t)(((int64_t)(M - 1) * ldx + K) * 2);
+    const uintptr_t we = wb + (uintptr_t)(((int64_t)(N - 1) * ldw + K) * 2);
+    const uintptr_t ye = yb + (uintptr_t)(((int64_t)(M - 1) * ldy + N) * 4);
+    if ((xb < ye && yb < xe) || (wb < ye && yb < we))
+      return fail(SIDON_E_SHAPE, "x and w must not overlap y (the kernel reads them while adding into y)");
+  }
   int rc;
   if ((rc = sidon::check_device())) return rc;
   ResParams p;

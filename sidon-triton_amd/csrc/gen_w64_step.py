@@ -2,13 +2,21 @@
 query rows per workgroup, two 32-row blocks per wavefront, two workgroups
 per compute unit) as hand-scheduled gfx950 assembly.
 
-Run by build.py before every compile.  Same arithmetic contract as
-gen_wide_step.py (whose instruction model, list scheduler and wait-state
-rules this reuses): every item computes exactly what the general code of
-flexrel_w64.hip computes for it, so the C++ rerun reproduces every query
-that did not overflow bit for bit.  Differences from the 128-row loop:
+Run by build.py before every compile (the instruction record, issue model,
+list scheduler and wait-state rules are gen_asm.py's).  The loop runs a
+wavefront's key steps in the kernel's processing order: the special steps
+first (band steps, where a block needs the per-score q.rel gather; the step
+straddling LK; the first step, which sets the running max exactly), then the
+plain steps (every block entirely left or entirely right of the window).
+Every item computes exactly what the general code of flexrel_w64.hip
+computes for it -- the same MFMAs on the same operands, the same fma / exp2 /
+fp16 rounding per score, the same row-sum accumulation -- so the C++ rerun
+(taken when a probability leaves the fp16 range) reproduces every query that
+did not overflow bit for bit.
 
-* two phases per key step (blocks 0 and 1);
+* two phases per key step (blocks 0 and 1); phase J of step j runs the PV
+  of item (j - 1, J), the softmax of item (j, J), the row sums of the
+  previous item and the score product of the next one;
 * K tiles pass through one LDS slot per wavefront into two register
   buffers: in phase 0 of step j, after the score product of item (j, 1)
   read K(j), K(j + 2) is read from the slot into that buffer, and then
@@ -42,8 +50,8 @@ import sys
 from pathlib import Path
 
 sys.path.insert(0, str(Path(__file__).resolve().parent))
-import gen_wide_step as G  # noqa: E402
-from gen_wide_step import (Ins, assert_quiet, branch, check_hazards, label, mfma16, mfma32, nop,  # noqa: E402
+import gen_asm as G  # noqa: E402
+from gen_asm import (Ins, assert_quiet, branch, check_hazards, label, mfma16, mfma32, nop,  # noqa: E402
                            salu, schedule, valu)
 
 OUT = Path(__file__).resolve().parent / "flexrel_w64_step.inc"
@@ -194,7 +202,12 @@ def gather_valu(J):
 
 
 def special_softmax(J, sl):
-    """As gen_wide_step.special_softmax, for block J of this layout."""
+    """Softmax of item (j, J) of a special step, after its bias gather, as
+    the general code forms it: y = s * scale + bias (masked keys -inf); at
+    the first step the running max from y (and the running sums scaled by
+    exp2(m_old - m_new)); then p = exp2(y - m) for band or masked items,
+    exp2(s * scale + (bias - m)) for plain ones.  Returns (text, path) where
+    path(needy, msk, first, gen) is the instruction sequence that runs."""
     bf = J
     s = SACC[bf]
     m = f"%[m{J}]"
@@ -245,7 +258,7 @@ def special_softmax(J, sl):
                         {f"v{pk(bf, hh) + r}"}))
     cvt.append(nop(1))
     for seq in (first, gen, plain, mask):
-        G._pad(seq)
+        G.pad(seq)
     text = (head + ys + chk_m + mask + [label(lab["nomask"])] + chk_f + first + [label(lab["noy"])] + chk_g + gen
             + [label(lab["plain"])] + plain + [label(lab["cvt"])] + cvt)
 
@@ -382,9 +395,13 @@ FENCE = G.FENCE
 
 
 def check_waits(seq, vm_outstanding):
-    """As gen_wide_step.check_waits, with register loads from global memory
-    (kind gload) in the vm queue: their registers may be read only after a
-    vmcnt wait retired them."""
+    """Outstanding-operation check: an LDS read result is used only after an
+    lgkmcnt wait retired it, a ring slot is read only after the vmcnt wait
+    that retires its copy, a slot is refilled only after the reads of its
+    previous contents retired, and the registers of a load from global
+    memory (kind gload) are read only after a vmcnt wait retired it.
+    vm_outstanding: (slot, registers) of the loads in flight at the start,
+    oldest first."""
     lgkm = []
     vm = []     # (slot, regs) per instruction in flight
     for slot, regs in vm_outstanding:

@@ -53,11 +53,8 @@ def test_launch_shape(sidon, B, H, L):
     s = sidon._lib.launch_shape(B, H, L)
     qpb = s["queries_per_block"]
     wgs = s["workgroups"]
-    assert qpb in (32, 64, 128)
-    if qpb in (32, 64):
-        assert wgs == B * H * -(-L // qpb)
-    else:
-        assert B * H * -(-L // 128) <= wgs <= B * H * -(-L // 64)
+    assert qpb in (32, 64)
+    assert wgs == B * H * -(-L // qpb)
     assert s["threads_per_block"] % 64 == 0
     assert s["key_splits"] >= 1
 
@@ -66,12 +63,12 @@ def test_shape_choice(sidon, monkeypatch):
     """The automatic choice: the 32-row kernel (4 key splits) while its
     workgroups fit one per compute unit and L <= 512, else the 64-row kernel with 4 key
     splits (two workgroups per compute unit); SIDON_FLEXREL_VARIANT forces
-    another, read at every call.  The 32-row kernel also needs L <= 1024 (its
-    compiled key steps cost more than the 64-row kernel's hand-scheduled ones).
-    Without a device the library assumes 256
-    compute units: H = 16 takes the 32-row kernel up to L = 512; forced
-    wide_tail runs c3 (608 blocks of 128 rows) as two whole rounds of
-    128-row blocks and the last 704 rows as 64-row blocks."""
+    another, read at every call, and an unknown value is an error
+    (SIDON_E_CONFIG) rather than a silent automatic choice.  The 32-row
+    kernel also needs L <= 1024 (its compiled key steps cost more than the
+    64-row kernel's hand-scheduled ones).  Without a device the library
+    assumes 256 compute units: H = 16 takes the 32-row kernel up to
+    L = 512."""
     monkeypatch.delenv("SIDON_FLEXREL_VARIANT", raising=False)
     for L in (150, 500, 512):
         s = sidon._lib.launch_shape(1, 16, L)
@@ -90,9 +87,16 @@ def test_shape_choice(sidon, monkeypatch):
     assert sidon._lib.launch_shape(1, 16, 150)["queries_per_block"] == 64
     monkeypatch.setenv("SIDON_FLEXREL_VARIANT", "w32")
     assert sidon._lib.launch_shape(1, 16, 4800)["workgroups"] == 16 * 150
-    monkeypatch.setenv("SIDON_FLEXREL_VARIANT", "wide_tail")
-    c3 = sidon._lib.launch_shape(1, 16, 4800)
-    assert c3["queries_per_block"] == 128 and c3["workgroups"] == 512 + 16 * 11
+    for name in ("wide", "W64", "w64 "):
+        monkeypatch.setenv("SIDON_FLEXREL_VARIANT", name)
+        with pytest.raises(RuntimeError, match="SIDON_E_CONFIG"):
+            sidon._lib.launch_shape(1, 16, 4800)
+        lib = sidon._lib.load()
+        assert lib.sidon_flexrel_launch_shape(1, 16, 4800, None, None, None, None) == -7
+        assert "SIDON_FLEXREL_VARIANT" in lib.sidon_last_error().decode()
+    for name in ("auto", ""):
+        monkeypatch.setenv("SIDON_FLEXREL_VARIANT", name)
+        assert sidon._lib.launch_shape(1, 16, 4800)["queries_per_block"] == 64
     monkeypatch.setenv("SIDON_FLEXREL_VARIANT", "split8")
     c1 = sidon._lib.launch_shape(1, 16, 750)
     assert c1["queries_per_block"] == 64 and c1["key_splits"] == 8 and c1["threads_per_block"] == 512
@@ -234,6 +238,10 @@ def test_residual_gemm_shape_support(sidon):
     (dict(ldy=1026), -3),
     (dict(x=24), -4),
     (dict(y=40), -4),
+    # y inside the bytes of x, or of w (the kernel reads them while adding into y)
+    (dict(x=1 << 30, w=1 << 31, y=(1 << 30) + 4096), -2),
+    (dict(x=1 << 30, w=1 << 31, y=(1 << 31) + 16), -2),
+    (dict(x=(1 << 30) + 16, w=1 << 31, y=1 << 30), -2),
 ])
 def test_residual_gemm_rejects_bad_arguments_before_launch(sidon, over, code):
     # fake aligned addresses, never dereferenced: validation returns before any HIP call

@@ -83,3 +83,30 @@ def test_summarize_counters_known_answer():
     assert math.isclose(res["traffic_over_algorithmic"], res["traffic_bytes"] / bench.ALGO_BYTES)
     # the c3 algorithmic bytes: q, k, v read and the output written once, the table, the length
     assert bench.ALGO_BYTES == 4 * 4800 * 1024 * 2 + 73 * 64 * 2 + 4
+
+
+def test_summarize_counters_mfma_busy_known_answer():
+    """Matrix-core occupancy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / 8)
+    / 1024 SIMDs, and the useful fraction = the launch's flops / (1024 flop
+    per SIMD-cycle x 1024 SIMDs x cycles).  Fabricated readings: 200 k cycles
+    per XCD and a busy count of half of 1024 x 200 k give 0.5."""
+    import bench
+
+    copy_kib = bench.COPY_PROBE_BYTES / 1024.0
+    names = {"1": "flexrel_w64_kernel", "2": "flexrel_w64_kernel", "3": "flexrel_w64_kernel"}
+    cyc = 200e3
+    fetch = {d: {"FETCH_SIZE": 1.0, "GRBM_GUI_ACTIVE": 8 * cyc} for d in names}
+    write = {d: {"WRITE_SIZE": 1.0, "GRBM_GUI_ACTIVE": 8 * cyc, "SQ_VALU_MFMA_BUSY_CYCLES": 0.5 * 1024 * cyc,
+                 "SQ_BUSY_CYCLES": 7.0} for d in names}
+    dur = {d: 1e5 for d in names}
+    cnames = {"7": "__amd_rocclr_copyBuffer"}
+    per = {"kernel_fetch": (fetch, names, dur), "kernel_write": (write, names, {}),
+           "copy_fetch": ({"7": {"FETCH_SIZE": copy_kib / 2}}, cnames, {}),
+           "copy_write": ({"7": {"WRITE_SIZE": copy_kib}}, cnames, {})}
+    res = bench.summarize_counters(per)
+    assert math.isclose(res["mfma_busy_frac"], 0.5)
+    assert math.isclose(res["cycles_per_launch"], cyc)
+    assert math.isclose(res["mfma_useful_frac"], bench.FLOPS_LAUNCH / 1024.0 / cyc / 1024.0)
+    # 95.09 GFLOP in 200 k cycles: 0.4534 of the matrix cores' capacity at that clock
+    assert math.isclose(res["mfma_useful_frac"], 0.4534, rel_tol=1e-3)
+    assert res["sq_busy_cycles"] == 7.0

@@ -71,6 +71,37 @@ def test_gemm_nt_untuned_default_matches_float64(sidon, monkeypatch):
     assert _rel(out, _reference(x, w, y0, 1.0)) <= TOL[torch.float32]
 
 
+def test_tuner_falls_back_to_the_default_kernel(sidon, monkeypatch):
+    """When no workspace-free kernel qualifies (forced here for every
+    problem), the tuner records rocBLAS's default and succeeds: the call runs
+    the default kernel, meets the float64 bar and equals an untuned call bit
+    for bit, and a second call does not time the problem again."""
+    import ctypes
+
+    monkeypatch.setenv("SIDON_GEMM_TUNE_FORCE_FALLBACK", "1")
+    x, w, y0 = _problem(1111, 640, 512, torch.float16, torch.float32, seed=11)
+    out = y0.clone()
+    sidon.blas.gemm_nt(x, w, out, beta=1.0)
+    torch.cuda.synchronize()
+    key = (DEV.index, 1111, 640, 512, x.stride(0), w.stride(0), out.stride(0), 2, True)
+    assert key in sidon.blas._tuned
+    assert sidon.blas._chosen[key] == -2 ** 31          # INT_MIN: rocBLAS's default
+    assert _rel(out, _reference(x, w, y0, 1.0)) <= TOL[torch.float32]
+    # the default without any tuning gives the same bits
+    lib = sidon._lib.load()
+    plain = y0.clone()
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    rc = lib.sidon_gemm_nt(x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0), plain.data_ptr(), plain.stride(0),
+                           1111, 640, 512, 2, 1.0, stream)
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert torch.equal(out, plain)
+    again = y0.clone()
+    sidon.blas.gemm_nt(x, w, again, beta=1.0)
+    torch.cuda.synchronize()
+    assert torch.equal(again, out)
+
+
 def test_gemm_nt_graph_replays_match_eager(sidon):
     """Two accumulating GEMMs captured into a HIP graph and replayed three
     times from the same start, with eager work and synchronisations between

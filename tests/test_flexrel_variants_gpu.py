@@ -2,9 +2,8 @@
 choice (needs an MI355X).
 
 `SIDON_FLEXREL_VARIANT` (read by the library at every call) forces the
-8-split kernel of flexrel_fwd.hip, the 128-row kernel of flexrel_wide.hip
-(alone, and as whole rounds plus an 8-split tail), the 64-row kernel of
-flexrel_w64.hip or the 32-row kernel of flexrel_w32.hip; K and V rows of
+8-split kernel of flexrel_fwd.hip, the 64-row kernel of flexrel_w64.hip or
+the 32-row kernel of flexrel_w32.hip; K and V rows of
 different strides take the 8-split kernel
 without being forced.  Each is checked against the float64 oracle at the
 north-star bar on ragged and padded shapes, for the same results contract:
@@ -24,7 +23,7 @@ from test_flexrel_gpu import DEV, assert_parity, run
 
 pytestmark = pytest.mark.gpu
 
-VARIANTS = ["split8", "wide", "wide_tail", "w64", "w32"]
+VARIANTS = ["split8", "w64", "w32"]
 SHAPES = [
     # (B, H, L, lens)
     (1, 2, 33, [20]),
@@ -74,9 +73,9 @@ def test_variant_padding_garbage_bit_identical(sidon, variant):
     assert torch.equal(got[:, :, :LK], got2[:, :, :LK]), f"{variant}: keys past LK changed valid rows"
 
 
-@pytest.mark.parametrize("variant", ["wide_tail", "w64", "w32"], indirect=True)
+@pytest.mark.parametrize("variant", ["w64", "w32"], indirect=True)
 def test_variant_c3_shape(sidon, variant):
-    """L=4800, H=16: the grids of several rounds (and the wide kernel's tail launch); 2 heads checked."""
+    """L=4800, H=16: the grids of several rounds; 2 heads checked."""
     q, k, v, rel = seeded_inputs(1, 16, 4800, seed=3)
     got = run(sidon, q, k, v, rel).float().cpu().numpy()
     assert np.isfinite(got).all()
@@ -114,7 +113,7 @@ def test_variant_fused_layout_l3000(sidon, variant):
     assert_parity(c["ref"][None], got, [L], f"{variant} fused L=3000")
 
 
-@pytest.mark.parametrize("variant", ["w64", "wide", "w32"], indirect=True)
+@pytest.mark.parametrize("variant", ["w64", "w32"], indirect=True)
 def test_variant_repeated_launches_bit_identical(sidon, variant):
     """200 launches on the same inputs give the same bits.  Regression test:
     the hand-scheduled loops once returned with their last V^T operand reads
