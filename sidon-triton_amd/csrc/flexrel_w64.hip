@@ -52,7 +52,14 @@ constexpr int kSlotStride = kWaves * kTile;      // 16 KB: V slot 0, V slot 1, K
 constexpr int kVSlot1 = kSlotStride;
 constexpr int kKSlot = 2 * kSlotStride;
 constexpr int kQrOff = 3 * kSlotStride;
-constexpr int kPreBytes = kQrOff + kRows * kQrStride * 4;
+// q.rel table rows: position p (0..72) at float kQrPad + p; floats
+// [0, kQrPad) repeat position 0 and [kQrPad + 73, kQrPad + 81) position 72,
+// so a run of 8 consecutive positions clamped to [0, 72] is 8 consecutive
+// floats of the row from the clamped start -- the band steps read a lane's
+// 16 biases as two such runs (ds_read2_b32).
+constexpr int kQrPad = 8;
+constexpr int kQrRow = 92;  // floats per row: kQrPad + 73 + 8, rounded up to 16 bytes
+constexpr int kPreBytes = kQrOff + kRows * kQrRow * 4;
 // Prologue staging, over regions the loop fills only after the q.rel table
 // is built: the Q block (64 rows) and rel rows 0-63 in the V slot 1 region,
 // rel rows 64-79 (row 72 repeated past it) after the table.
@@ -229,7 +236,8 @@ flexrel_w64_kernel(const Params p) {
   // q.rel^T * scale for the 64 rows, as twenty (16 positions x 16 rows)
   // tiles rel . Q^T of v_mfma_f32_16x16x32_f16: wavefront w takes rows
   // 16 w + [0, 16) and all five position blocks (positions 0-79; rel rows
-  // >= 73 are 0, positions >= 76 are not stored) -- five independent
+  // >= 73 are 0; positions 73-79 are not stored: the row's padding repeats
+  // position 72 there, and position 0 before it) -- five independent
   // two-product chains per wavefront.  Lane l supplies position (A) and row
   // (B) l % 16, dims 32 t + 8 (l / 16) + [0, 8) of k-step t, and receives
   // positions 4 (l / 16) + [0, 4) of row l % 16.
@@ -260,12 +268,25 @@ flexrel_w64_kernel(const Params p) {
         acc[pb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(e, qb[t], acc[pb], 0, 0, 0);
       }
     }
+    float* qrow = qr_tab + qr * kQrRow + kQrPad;  // position 0 of row qr
 #pragma unroll
     for (int pb = 0; pb < 5; ++pb) {
       const int pos0 = 16 * pb + 4 * kg;
-      if (pos0 < kQrStride) {
+      if (pos0 + 3 < kNumPos - 1) {
         const f4 val = {acc[pb][0] * scale, acc[pb][1] * scale, acc[pb][2] * scale, acc[pb][3] * scale};
-        *reinterpret_cast<f4*>(qr_tab + qr * kQrStride + pos0) = val;
+        *reinterpret_cast<f4*>(qrow + pos0) = val;
+      } else if (pos0 == kNumPos - 1) {  // position 72 and the padding after it
+        const float e = acc[pb][0] * scale;
+        const f4 val = {e, e, e, e};
+        *reinterpret_cast<f4*>(qrow + pos0) = val;
+        *reinterpret_cast<f4*>(qrow + pos0 + 4) = val;
+        qrow[pos0 + 8] = e;
+      }
+      if (pos0 == 0) {  // the padding before position 0
+        const float e = acc[pb][0] * scale;
+        const f4 val = {e, e, e, e};
+        *reinterpret_cast<f4*>(qrow - 8) = val;
+        *reinterpret_cast<f4*>(qrow - 4) = val;
       }
     }
   }
@@ -359,7 +380,7 @@ flexrel_w64_kernel(const Params p) {
     const float off = left ? ql[J] : (right ? qrr[J] : 0.f);
     float y[16];
     if (band) {
-      const float* qrow = qr_tab + (32 * J + n) * kQrStride;
+      const float* qrow = qr_tab + (32 * J + n) * kQrRow + kQrPad;
       const int d0 = k0 + 8 * g - (qlo + n) + kLeft;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
@@ -448,8 +469,8 @@ flexrel_w64_kernel(const Params p) {
         float ql[kBlocks], qrr[kBlocks];
 #pragma unroll
         for (int J = 0; J < kBlocks; ++J) {
-          ql[J] = qr_tab[(32 * J + t1.n) * kQrStride];
-          qrr[J] = qr_tab[(32 * J + t1.n) * kQrStride + kNumPos - 1];
+          ql[J] = qr_tab[(32 * J + t1.n) * kQrRow + kQrPad];
+          qrr[J] = qr_tab[(32 * J + t1.n) * kQrRow + kQrPad + kNumPos - 1];
         }
 #pragma unroll
         for (int J = 0; J < kBlocks; ++J) {
@@ -501,7 +522,7 @@ flexrel_w64_kernel(const Params p) {
       for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
         for (int db = 0; db < 2; ++db) tv[hf][db] = ring_lds + (uint32_t)lt.tr_off[hf][db];
-      const uint32_t qbase_lds = (uint32_t)(uintptr_t)SIDON_LDS_PTR(float, qr_tab + n * kQrStride);
+      const uint32_t qbase_lds = (uint32_t)(uintptr_t)SIDON_LDS_PTR(float, qr_tab + n * kQrRow + kQrPad);
       const int laned = 8 * g - n;
       const int g8 = 8 * g;
       // (The loop writes M0 for its LDS copies; the clobber says so.  The
@@ -531,7 +552,7 @@ flexrel_w64_kernel(const Params p) {
                      [ko1] "v"(lt.voff[1]), [ko2] "v"(lt.voff[2]), [ko3] "v"(lt.voff[3]), [kl0] "v"(lt.voff_last[0]),
                      [kl1] "v"(lt.voff_last[1]), [kl2] "v"(lt.voff_last[2]), [kl3] "v"(lt.voff_last[3]),
                      [ka0] "v"(ka[0]), [ka1] "v"(ka[1]), [ka2] "v"(ka[2]), [ka3] "v"(ka[3]), [tv00] "v"(tv[0][0]), [tv01] "v"(tv[0][1]),
-                     [tv10] "v"(tv[1][0]), [tv11] "v"(tv[1][1]), [qbase] "v"(qbase_lds), [qhi] "v"(qbase_lds + 4 * (kNumPos - 1)), [laned] "v"(laned),
+                     [tv10] "v"(tv[1][0]), [tv11] "v"(tv[1][1]), [qbase] "v"(qbase_lds), [laned] "v"(laned),
                      [g8] "v"(g8)
                    : SIDON_W64_VGPR_CLOBBERS, SIDON_W64_SGPR_CLOBBERS, "vcc", "m0", "scc", "memory");
 #pragma clang diagnostic pop

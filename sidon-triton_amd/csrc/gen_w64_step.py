@@ -66,7 +66,8 @@ S_J, S_NU, S_JUMP, S_RING, S_SCALE, S_T = 64, 65, 66, 67, 68, 69
 S_GK, S_GV, S_DSTEP, S_DJUMP, S_D = 70, 72, 74, 76, 78
 S_GEN, S_MSK, S_NEEDY, S_DU, S_LIM = 80, 81, 82, 83, 85   # S_DU: two
 S_TMP = 87        # s87..s95
-QR_BLOCK = 32 * 76 * 4
+QR_ROW = 92 * 4      # bytes per q.rel row: 8 floats of padding (position 0), 73 positions, padding (72)
+QR_BLOCK = 32 * QR_ROW
 VGPR_CLOBBERS = [f"v{r}" for r in range(T0, X0 + 5)]
 SGPR_CLOBBERS = ["s69", "s78", "s79"] + [f"s{r}" for r in range(80, 96)]
 
@@ -181,23 +182,40 @@ def key_col(i):
 
 
 def gather_valu(J):
-    """LDS reads of the 16 biases of a band item: byte address = the lane's
-    q.rel row (qbase) + 4 (d0 + key column), clamped to [qbase, qhi] =
-    [qbase, qbase + 4 * 72] by one v_med3 (the clamp of the position to
-    [0, 72]): two vector instructions per bias."""
+    """LDS reads of the 16 biases of a band item.  The lane's keys are the
+    runs d0 + [0, 8) and d0 + 16 + [0, 8) of positions (d0 = k0 + 8 g -
+    (q0 + 32 J + n) + 64), each clamped to [0, 72]; the q.rel row repeats
+    position 0 in the 8 floats before it and position 72 in the 8 after it,
+    so each run is 8 consecutive floats of the row from its clamped start
+    s' = clamp(s, -8, 72) -- formed as clamp(s - 8, -16, 64) (both bounds
+    inline constants) -- read by four ds_read2_b32.  Addresses in t7 and t15
+    (each the last destination of its run's reads) and x0."""
     d = valu(f"v_add_u32_e32 {x(0)}, s{S_DU + J}, %[laned]", (), {x(0)}, f"D.{J}")
-    b = valu(f"v_lshl_add_u32 {x(0)}, {x(0)}, 2, %[qbase]", {x(0)}, {x(0)}, f"B.{J}")
-    b.deps = [d.tag]
-    out = [d, b]
-    for i in range(16):
-        a = valu(f"v_add_u32_e32 {t(i)}, {4 * key_col(i)}, {x(0)}", {x(0)}, {t(i)}, f"A{i}.{J}")
-        a.deps = [b.tag]
-        m = valu(f"v_med3_i32 {t(i)}, {t(i)}, %[qbase], %[qhi]", {t(i)}, {t(i)}, f"M{i}.{J}")
+    out = [d]
+    adr = []
+    for h in range(2):
+        r = t(8 * h + 7)
+        a = valu(f"v_add_u32_e32 {r}, {16 * h - 8}, {x(0)}", {x(0)}, {r}, f"A{h}.{J}")
+        a.deps = [d.tag]
+        m = valu(f"v_med3_i32 {r}, {r}, -16, 64", {r}, {r}, f"M{h}.{J}")
         m.deps = [a.tag]
-        rd = Ins(f"ds_read_b32 {t(i)}, {t(i)} offset:{QR_BLOCK * J}", "lds", reads={t(i)}, writes={t(i)},
-                 tag=f"G{i}.{J}")
-        rd.deps = [m.tag]
-        out += [a, m, rd]
+        out += [a, m]
+        adr.append(r)
+    # the row's position 0 (block J) + 4 x 8: the byte address of s' is base + 4 (s - 8)
+    base = valu(f"v_add_u32_e32 {x(0)}, {QR_BLOCK * J + 32}, %[qbase]", (), {x(0)}, f"Q.{J}")
+    base.deps = ["A0." + str(J), "A1." + str(J)]
+    out.append(base)
+    for h in range(2):
+        r = adr[h]
+        sh = valu(f"v_lshl_add_u32 {r}, {r}, 2, {x(0)}", {r, x(0)}, {r}, f"L{h}.{J}")
+        sh.deps = [f"M{h}.{J}", base.tag]
+        out.append(sh)
+        for k in range(4):
+            i = 8 * h + 2 * k
+            rd = Ins(f"ds_read2_b32 v[{T0 + i}:{T0 + i + 1}], {r} offset0:{2 * k} offset1:{2 * k + 1}", "lds",
+                     reads={r}, writes={t(i), t(i + 1)}, tag=f"G{i}.{J}")
+            rd.deps = [sh.tag] + ([f"G{i - 2}.{J}"] if k else [])
+            out.append(rd)
     return out
 
 
