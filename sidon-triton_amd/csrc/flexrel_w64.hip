@@ -316,11 +316,22 @@ flexrel_w64_kernel(const Params p) {
       }
     }
   };
-  auto qk = [&](int J, const h8 (&k)[4]) SIDON_INLINE {
+  auto qk_with = [&](const h8 (&qo)[4], const h8 (&k)[4]) SIDON_INLINE {
     f32x16 acc = {};
 #pragma unroll
-    for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(k[s], qop[J][s], acc, 0, 0, 0);
+    for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(k[s], qo[s], acc, 0, 0, 0);
     return acc;
+  };
+  auto qk = [&](int J, const h8 (&k)[4]) SIDON_INLINE { return qk_with(qop[J], k); };
+  // Q^T operands of block J read again from global memory (the rerun: the
+  // staged Q block in LDS is overwritten by then), with the same values as
+  // qop: lane (n, g) holds query q0 + 32 J + n, dims 16 s + 8 g + [0, 8);
+  // rows >= L are 0.
+  auto load_q = [&](const LaneTab& t, int J, h8 (&dst)[4]) SIDON_INLINE {
+    const int row = q0 + 32 * J + t.n;
+    const _Float16* src = qbase + (int64_t)min(row, p.L - 1) * p.qsl + 8 * t.g;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) dst[s] = row < p.L ? *reinterpret_cast<const h8*>(src + 16 * s) : h8{};
   };
   auto pv = [&](int J, int bf) SIDON_INLINE {
 #pragma unroll
@@ -341,10 +352,13 @@ flexrel_w64_kernel(const Params p) {
   const _Float16 sel_v = (((lane >> 4) ^ (lane >> 2)) & 1) == 0 ? (_Float16)1 : (_Float16)0;
   h8 sel = {sel_v, sel_v, sel_v, sel_v, sel_v, sel_v, sel_v, sel_v};
   asm volatile("" : "+v"(sel));
+  auto accumulate_with = [&](const h8& sl, int J, int bf) SIDON_INLINE {
+    lsum[J] = __builtin_amdgcn_mfma_f32_16x16x32_f16(sl, pk[bf][0], lsum[J], 0, 0, 0);
+    lsum[J] = __builtin_amdgcn_mfma_f32_16x16x32_f16(sl, pk[bf][1], lsum[J], 0, 0, 0);
+  };
   auto accumulate = [&](int J, int bf) SIDON_INLINE {
     asm volatile("" : "+v"(sel));
-    lsum[J] = __builtin_amdgcn_mfma_f32_16x16x32_f16(sel, pk[bf][0], lsum[J], 0, 0, 0);
-    lsum[J] = __builtin_amdgcn_mfma_f32_16x16x32_f16(sel, pk[bf][1], lsum[J], 0, 0, 0);
+    accumulate_with(sel, J, bf);
   };
 
   auto emit = [&](int bf, int i, const f2& e) SIDON_INLINE {
@@ -367,7 +381,7 @@ flexrel_w64_kernel(const Params p) {
   // change the rounding of another.  A query that needs no update keeps its
   // max, and its probabilities are the ones the hand-scheduled loop forms.
   auto item = [&](const LaneTab& t, const float (&ql)[kBlocks], const float (&qrr)[kBlocks], int j, int u,
-                  int J) SIDON_INLINE {
+                  int J, int sb) SIDON_INLINE {
     const int n = t.n, g = t.g;
     int k0 = (w + kWaves * u) * kStep;
     asm volatile("" : "+s"(k0));
@@ -385,11 +399,11 @@ flexrel_w64_kernel(const Params p) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int idx = min(max(d0 + 16 * (i >> 3) + (i & 7), 0), kLeft + kRight);
-        y[i] = fmaf(sacc[0][i], scale, qrow[idx]);
+        y[i] = fmaf(sacc[sb][i], scale, qrow[idx]);
       }
     } else {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) y[i] = fmaf(sacc[0][i], scale, off);
+      for (int i = 0; i < 16; ++i) y[i] = fmaf(sacc[sb][i], scale, off);
     }
     if (masked) {
 #pragma unroll
@@ -401,9 +415,9 @@ flexrel_w64_kernel(const Params p) {
     auto probs = [&](float m) SIDON_INLINE {
       if (band || masked) {
 #pragma unroll
-        for (int i = 0; i < 16; i += 2) emit(0, i, f2{fast_exp2(y[i] - m), fast_exp2(y[i + 1] - m)});
+        for (int i = 0; i < 16; i += 2) emit(sb, i, f2{fast_exp2(y[i] - m), fast_exp2(y[i + 1] - m)});
       } else {  // the plain form, bit for bit as the loop computes it
-        probs_fast(0, off - m);
+        probs_fast(sb, off - m);
       }
     };
     bool need = first;
@@ -413,7 +427,7 @@ flexrel_w64_kernel(const Params p) {
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) own += (float)pk[0][hh][e];
+        for (int e = 0; e < 8; ++e) own += (float)pk[sb][hh][e];
       const auto pr = __builtin_amdgcn_permlane32_swap(__float_as_uint(own), __float_as_uint(own), false, false);
       need = !(__uint_as_float(pr[0]) + __uint_as_float(pr[1]) < INFINITY);
     }
@@ -464,14 +478,6 @@ flexrel_w64_kernel(const Params p) {
     // its steps again through `item` above, one step at a time.
     for (bool safe = false;; safe = true) {
       if (safe) {
-        // every lane-dependent value formed again (none survives the loop)
-        const LaneTab t1 = lane_tab(fresh_lane_id(), kstride, last_row);
-        float ql[kBlocks], qrr[kBlocks];
-#pragma unroll
-        for (int J = 0; J < kBlocks; ++J) {
-          ql[J] = qr_tab[(32 * J + t1.n) * kQrRow + kQrPad];
-          qrr[J] = qr_tab[(32 * J + t1.n) * kQrRow + kQrPad + kNumPos - 1];
-        }
 #pragma unroll
         for (int J = 0; J < kBlocks; ++J) {
           oacc[J][0] = f32x16{};
@@ -480,21 +486,40 @@ flexrel_w64_kernel(const Params p) {
           lsum[J] = f32x4{};
         }
         for (int j = 0; j < nu; ++j) {
+          // every lane-dependent value formed again at every step (none
+          // survives the hand-scheduled loop, and none is kept across the
+          // steps here: with the accumulators, Q^T and the row state live,
+          // keeping the lane offsets too spilled them to scratch, and a
+          // scratch segment slows every launch, rerun or not)
+          const LaneTab t1 = lane_tab(fresh_lane_id(), kstride, last_row);
+          float ql[kBlocks], qrr[kBlocks];
+#pragma unroll
+          for (int J = 0; J < kBlocks; ++J) {
+            ql[J] = qr_tab[(32 * J + t1.n) * kQrRow + kQrPad];
+            qrr[J] = qr_tab[(32 * J + t1.n) * kQrRow + kQrPad + kNumPos - 1];
+          }
           const int u = u_of(j);
-          load_k(t1, j, kop[0]);
+          const int ln = t1.n + 32 * t1.g;
+          const _Float16 sv = (((ln >> 4) ^ (ln >> 2)) & 1) == 0 ? (_Float16)1 : (_Float16)0;
+          const h8 sel1 = {sv, sv, sv, sv, sv, sv, sv, sv};
           wait_lgkm0();  // the reads of the previous V tile are done
           copy_v(t1, j, ring_lds, vbase);
           wait_vmcnt<0>();
           load_v(t1, 0);
 #pragma unroll
           for (int J = 0; J < kBlocks; ++J) {
-            sacc[0] = qk(J, kop[0]);
+            // the K and Q^T operands read for each block (only one block's
+            // are live at a time)
+            h8 ko[4], qo[4];
+            load_k(t1, j, ko);
+            load_q(t1, J, qo);
+            sacc[0] = qk_with(qo, ko);
             // (every item, the plain ones too: their probabilities take the
             // loop's plain form, and a query past the fp16 range must not
             // reach the row-sum product, where its inf would turn the sum of
             // the other query of its lane group into NaN)
-            item(t1, ql, qrr, j, u, J);
-            accumulate(J, 0);
+            item(t1, ql, qrr, j, u, J, 0);
+            accumulate_with(sel1, J, 0);
             pv(J, 0);
           }
         }
