@@ -61,14 +61,14 @@ def test_launch_shape(sidon, B, H, L):
 
 def test_shape_choice(sidon, monkeypatch):
     """The automatic choice: the 32-row kernel (4 key splits) while its
-    workgroups fit one per compute unit and L <= 512, else the 64-row kernel with 4 key
-    splits (two workgroups per compute unit); SIDON_FLEXREL_VARIANT forces
-    another, read at every call, and an unknown value is an error
-    (SIDON_E_CONFIG) rather than a silent automatic choice.  The 32-row
-    kernel also needs L <= 1024 (its compiled key steps cost more than the
-    64-row kernel's hand-scheduled ones).  Without a device the library
-    assumes 256 compute units: H = 16 takes the 32-row kernel up to
-    L = 512."""
+    B H ceil(L / 32) workgroups fit one per compute unit and L <= 1024 (its
+    compiled key steps cost more than the 64-row kernel's hand-scheduled
+    ones), else the 64-row kernel with 4 key splits (two workgroups per
+    compute unit); SIDON_FLEXREL_VARIANT forces another, read at every call,
+    and an unknown value is an error (SIDON_E_CONFIG) rather than a silent
+    automatic choice.  Without a device the library assumes 256 compute
+    units: H = 16 then takes the 32-row kernel up to L = 512 (the compute
+    unit limit), H = 4 up to L = 1024 (the key limit)."""
     monkeypatch.delenv("SIDON_FLEXREL_VARIANT", raising=False)
     for L in (150, 500, 512):
         s = sidon._lib.launch_shape(1, 16, L)
