@@ -134,26 +134,28 @@ int sidon_gemm_res(const void* x, int ldx, const void* w, int ldw, float* y, int
  * sidon_gemm_nt runs the kernel recorded for the problem (shape, strides,
  * dtype, beta != 0) by sidon_gemm_nt_tune or sidon_gemm_nt_pin, else
  * rocBLAS's default.  The tuner times rocBLAS's default and every solution
- * it lists for the problem that needs no workspace (rocBLAS's device-memory
- * size query), on scratch: y and y_check are two distinct buffers of y's
+ * it lists for the problem, on scratch: y and y_check are two distinct buffers of y's
  * shape and row stride (both overwritten; y's contents are the beta term
  * while timing).  It records for the current device the fastest kernel whose
  * product agrees with the default's -- at beta = 0 and, when beta != 0, with
  * the problem's beta from identical contents; fp32 output: every row and
  * column within 1e-5 relative; fp16 output: every element within one fp16
  * ulp and the whole within 1e-4 -- and writes its solution index to
- * *solution_out (INT_MIN: the default) when that is not NULL.  When no
- * listed kernel is free of workspace or none passes that gate, it records
+ * *solution_out (INT_MIN: the default) when that is not NULL.  When rocBLAS
+ * lists no kernel or none passes that gate, it records
  * rocBLAS's default and returns SIDON_OK (SIDON_GEMM_TUNE_FORCE_FALLBACK=1
- * takes that path for every problem, for tests).  The tuner
+ * takes that path for every problem, for tests).  Each candidate's timed
+ * calls are queued behind a short hold kernel (one lane, 400 us) so that
+ * they run back to back on the device and its own speed is measured, not
+ * the host's launch rate.  The tuner
  * synchronises the stream and fails during stream capture; tune before
  * capturing.  Every candidate is deterministic (rocBLAS atomics disabled),
  * but the choice is by timing, so two processes may keep different kernels
  * (outputs differing in the last bits).  Each device's rocBLAS handle gets a
  * fixed 32 MiB workspace, allocated on the first call on that device and
- * never freed, so graphs never point at memory rocBLAS has freed; only
- * rocBLAS's default kernel of an untuned problem may use it, and such calls
- * on two streams of one device must not overlap.  Neither function has a
+ * never freed, so graphs never point at memory rocBLAS has freed; any kernel
+ * may use it (rocBLAS answers no workspace-size query for these GEMMs), so
+ * calls on two streams of one device must not overlap.  Neither function has a
  * counterpart in the reference.
  */
 int sidon_gemm_nt(const void* x, int ldx, const void* w, int ldw, void* y, int ldy, int M, int N, int K, int dtype,
@@ -165,8 +167,9 @@ int sidon_gemm_nt_tune(const void* x, int ldx, const void* w, int ldw, void* y, 
  * in an earlier run; INT_MIN = rocBLAS's default) for the problem
  * (M, N, K, ldx, ldw, ldy, dtype, beta != 0) on the current device, so runs
  * are reproducible.  The first sidon_gemm_nt call of the problem fails with
- * SIDON_E_SHAPE if rocBLAS has no such kernel for it or the kernel needs a
- * workspace.  No counterpart in the reference.
+ * SIDON_E_SHAPE, before running anything, if rocBLAS does not list the kernel
+ * for this exact problem (shape, strides, types).  No counterpart in the
+ * reference.
  */
 int sidon_gemm_nt_pin(int M, int N, int K, int ldx, int ldw, int ldy, int dtype, int beta_nonzero,
                       int solution);

@@ -21,8 +21,9 @@ scratch tensors shaped like ``out`` and keeps the fastest one whose product
 agrees with rocBLAS's default (``sidon_gemm_nt_tune``; the scratch lives only
 for that call).  Later calls, and calls during capture, launch the kept
 kernel, or rocBLAS's default before a problem is tuned.  Every candidate is
-deterministic and needs no workspace.  SIDON_GEMM_TUNE=0 in the environment
-keeps rocBLAS's default kernels.
+deterministic; any kernel may use the device's fixed rocBLAS workspace, so
+calls on two streams of one device must not overlap.  SIDON_GEMM_TUNE=0 in
+the environment keeps rocBLAS's default kernels.
 
 The choice is made by timing, so two processes (or boxes) may keep different
 kernels whose outputs differ in the last bits: results are not
@@ -30,7 +31,8 @@ bit-reproducible across processes while tuning is on.  ``chosen_kernels()``
 returns the kernel kept per problem, and SIDON_GEMM_PIN=<file.json> (a map
 from ``problem_name(key)`` to a rocBLAS solution index, e.g. written from
 ``chosen_kernels()`` of an earlier run) pins those problems to the given
-kernels instead of timing them.
+kernels instead of timing them; a kernel rocBLAS does not list for the
+problem is refused on its first call.
 """
 
 from __future__ import annotations

@@ -19,11 +19,10 @@
 // Device memory.  Each device's handle gets a fixed workspace of
 // kWorkspaceBytes that this library allocates once and never frees, so
 // rocBLAS never reallocates (and frees) memory that a captured graph still
-// points to.  The tuner keeps only kernels that need no workspace at all
-// (rocBLAS's device-memory size query), so a tuned problem shares no memory
-// between streams; only rocBLAS's default kernel of an untuned problem may
-// use the workspace, and such calls on two streams of one device must not
-// overlap.
+// points to.  Any kernel may use that workspace (rocBLAS's device-memory size
+// query does not apply to rocblas_gemm_ex: inside it the call runs as usual
+// and reports no size, so a kernel's need cannot be asked without running
+// it), so calls on two streams of one device must not overlap.
 //
 // The kept kernel is chosen by timing, so two processes may keep different
 // kernels whose outputs differ in the last bits; sidon_gemm_nt_pin records a
@@ -78,7 +77,7 @@ std::mutex g_mu;  // guards the handles (one stream binding at a time) and the t
 rocblas_handle g_handle[kMaxDevices] = {};
 void* g_workspace[kMaxDevices] = {};  // held until the process ends
 std::map<Key, int> g_choice;
-std::set<Key> g_checked;  // problems whose recorded kernel needs no workspace
+std::set<Key> g_checked;  // problems whose recorded kernel rocBLAS lists for them
 
 rocblas_datatype in_type(int dtype) { return dtype == 0 ? rocblas_datatype_f32_r : rocblas_datatype_f16_r; }
 rocblas_datatype out_type(int dtype) { return dtype == 1 ? rocblas_datatype_f16_r : rocblas_datatype_f32_r; }
@@ -108,6 +107,16 @@ int handle_for(int dev, rocblas_handle* h) {
   return SIDON_OK;
 }
 
+// Holds its stream for `ticks` of the constant-rate wall clock.  The tuner
+// queues the calls it times behind it, so that they run back to back once it
+// ends: at a few microseconds per kernel, calls issued one by one from the
+// host are spaced by the host's launch cost, which would be timed instead of
+// the kernel.  One lane; bounded by `ticks`.
+__global__ void hold_kernel(long long ticks) {
+  const long long t0 = wall_clock64();
+  while (wall_clock64() - t0 < ticks) __builtin_amdgcn_s_sleep(8);
+}
+
 rocblas_status run(rocblas_handle h, const Problem& p, int solution) {
   const float one = 1.f;
   const bool dflt = solution == kDefault;
@@ -118,16 +127,25 @@ rocblas_status run(rocblas_handle h, const Problem& p, int solution) {
                          rocblas_gemm_flags_none);
 }
 
-// Device memory (bytes) kernel `solution` needs for p, from rocBLAS's size
-// query (the call is not executed); SIZE_MAX when the query fails.
-size_t workspace_need(rocblas_handle h, const Problem& p, int solution) {
-  size_t bytes = SIZE_MAX;
-  if (rocblas_start_device_memory_size_query(h) != rocblas_status_success) return SIZE_MAX;
-  const rocblas_status st = run(h, p, solution);
-  if (rocblas_stop_device_memory_size_query(h, &bytes) != rocblas_status_success ||
-      (st != rocblas_status_success && st != rocblas_status_size_unchanged && st != rocblas_status_size_increased))
-    return SIZE_MAX;
-  return bytes;
+// The kernels rocBLAS lists for problem p (its solution predicates cover the
+// shape, strides and types; a kernel is only run on a problem that lists
+// it).  Empty when the query fails.
+std::vector<int> listed_solutions(rocblas_handle h, const Problem& p) {
+  const float one = 1.f;
+  rocblas_int n = 0;
+  auto list = [&](rocblas_int* out) {
+    return rocblas_gemm_ex_get_solutions(h, rocblas_operation_transpose, rocblas_operation_none, p.N, p.M, p.K, &one,
+                                         p.w, in_type(p.dtype), p.ldw, p.x, in_type(p.dtype), p.ldx, &p.beta, p.y,
+                                         out_type(p.dtype), p.ldy, p.y, out_type(p.dtype), p.ldy,
+                                         rocblas_datatype_f32_r, rocblas_gemm_algo_solution_index,
+                                         rocblas_gemm_flags_none, out, &n);
+  };
+  std::vector<int> ids;
+  if (list(nullptr) == rocblas_status_success && n > 0) {
+    std::vector<rocblas_int> raw(n);
+    if (list(raw.data()) == rocblas_status_success) ids.assign(raw.begin(), raw.end());
+  }
+  return ids;
 }
 
 int validate(const Problem& p) {
@@ -267,9 +285,10 @@ SIDON_API int sidon_gemm_nt(const void* x, int ldx, const void* w, int ldw, void
   const auto it = g_choice.find(key);
   const int solution = it == g_choice.end() ? kDefault : it->second;
   if (solution != kDefault && g_checked.count(key) == 0) {  // a pinned kernel, first call
-    const size_t need = workspace_need(h, p, solution);
-    if (need == SIZE_MAX) return fail(SIDON_E_SHAPE, "rocBLAS has no kernel %d for this problem", solution);
-    if (need != 0) return fail(SIDON_E_SHAPE, "kernel %d needs %zu bytes of workspace", solution, need);
+    const std::vector<int> ids = listed_solutions(h, p);
+    if (std::find(ids.begin(), ids.end(), solution) == ids.end())
+      return fail(SIDON_E_SHAPE, "rocBLAS does not list kernel %d for this problem (shape, strides, types)",
+                  solution);
     g_checked.insert(key);
   }
   if (rocblas_set_stream(h, reinterpret_cast<hipStream_t>(stream)) != rocblas_status_success)
@@ -301,39 +320,15 @@ SIDON_API int sidon_gemm_nt_tune(const void* x, int ldx, const void* w, int ldw,
 
   // Candidates: rocBLAS's default, then every listed solution.
   std::vector<int> cand{kDefault};
-  {
-    const float one = 1.f;
-    rocblas_int n = 0;
-    auto list = [&](rocblas_int* out) {
-      return rocblas_gemm_ex_get_solutions(h, rocblas_operation_transpose, rocblas_operation_none, p.N, p.M, p.K,
-                                           &one, p.w, in_type(p.dtype), p.ldw, p.x, in_type(p.dtype), p.ldx,
-                                           &p.beta, p.y, out_type(p.dtype), p.ldy, p.y, out_type(p.dtype), p.ldy,
-                                           rocblas_datatype_f32_r, rocblas_gemm_algo_solution_index,
-                                           rocblas_gemm_flags_none, out, &n);
-    };
-    if (list(nullptr) == rocblas_status_success && n > 0) {
-      std::vector<rocblas_int> ids(n);
-      if (list(ids.data()) == rocblas_status_success)
-        for (rocblas_int i = 0; i < n; ++i) cand.push_back(ids[i]);
-    }
-  }
+  for (const int c : listed_solutions(h, p)) cand.push_back(c);
 
-  // Only kernels that need no device memory beyond their operands: a kernel
-  // that used the handle's workspace would share it between streams.
-  {
-    std::vector<int> kept;
-    for (const int c : cand)
-      if (workspace_need(h, p, c) == 0) kept.push_back(c);
-    cand.swap(kept);
-  }
   // SIDON_GEMM_TUNE_FORCE_FALLBACK=1 (tests) treats every candidate as
   // unusable, which takes the fallback below.
   const char* force = getenv("SIDON_GEMM_TUNE_FORCE_FALLBACK");
   if (force != nullptr && strcmp(force, "1") == 0) cand.clear();
-  // When no workspace-free kernel is left, or none passes the accuracy gate
-  // below, the problem keeps rocBLAS's default: it is always valid
-  // (sidon_gemm_nt runs it with the handle's fixed workspace), and the
-  // problem counts as tuned, so later calls do not time it again.
+  // When no candidate is left, or none passes the accuracy gate below, the
+  // problem keeps rocBLAS's default: it is always valid, and the problem
+  // counts as tuned, so later calls do not time it again.
   auto keep_default = [&]() {
     g_choice[key_of(dev, p)] = kDefault;
     g_checked.insert(key_of(dev, p));
@@ -348,18 +343,30 @@ SIDON_API int sidon_gemm_nt_tune(const void* x, int ldx, const void* w, int ldw,
     return fail(SIDON_E_LAUNCH, "hipEventCreate failed");
   }
   // Each candidate: two untimed runs, then the best of two timed groups of
-  // four (the minimum is the least disturbed estimate of its speed).
+  // kGroup calls (the minimum is the least disturbed estimate of its speed),
+  // each group queued behind a hold of kHoldUs so that its calls run back to
+  // back on the device.
+  constexpr int kGroup = 8;
+  constexpr int kHoldUs = 400;
+  int clock_khz = 0;
+  if (hipDeviceGetAttribute(&clock_khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess || clock_khz <= 0) {
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    return fail(SIDON_E_LAUNCH, "wall clock rate query failed on device %d", dev);
+  }
+  const long long hold_ticks = (long long)clock_khz * kHoldUs / 1000;
   std::vector<std::pair<float, int>> timed;  // (us per call, candidate)
   for (const int c : cand) {
     bool ok = run(h, p, c) == rocblas_status_success && run(h, p, c) == rocblas_status_success;
     float us = 1e30f;
     for (int rep = 0; ok && rep < 2; ++rep) {
-      ok = ok && hipEventRecord(e0, s) == hipSuccess;
-      for (int i = 0; i < 4; ++i) ok = ok && run(h, p, c) == rocblas_status_success;
+      hipLaunchKernelGGL(hold_kernel, dim3(1), dim3(1), 0, s, hold_ticks);
+      ok = ok && hipGetLastError() == hipSuccess && hipEventRecord(e0, s) == hipSuccess;
+      for (int i = 0; i < kGroup; ++i) ok = ok && run(h, p, c) == rocblas_status_success;
       ok = ok && hipEventRecord(e1, s) == hipSuccess;
       float ms = 0.f;
       if (!ok || hipEventSynchronize(e1) != hipSuccess || hipEventElapsedTime(&ms, e0, e1) != hipSuccess) ok = false;
-      if (ms * 250.f < us) us = ms * 250.f;  // 1000 us / 4 calls
+      if (ms * 1000.f / kGroup < us) us = ms * 1000.f / kGroup;
     }
     if (ok) timed.emplace_back(us, c);
   }
@@ -425,8 +432,8 @@ SIDON_API int sidon_gemm_nt_pin(int M, int N, int K, int ldx, int ldw, int ldy, 
     g_choice[key] = kDefault;
     return SIDON_OK;
   }
-  // Checked on the first call of the problem (sidon_gemm_nt): the kernel
-  // must exist for it and need no workspace.
+  // Checked on the first call of the problem (sidon_gemm_nt): rocBLAS must
+  // list the kernel for it.
   g_checked.erase(key);
   g_choice[key] = solution;
   return SIDON_OK;
