@@ -17,6 +17,9 @@ did not overflow bit for bit.
 * two phases per key step (blocks 0 and 1); phase J of step j runs the PV
   of item (j - 1, J), the softmax of item (j, J), the row sums of the
   previous item and the score product of the next one;
+* a phase of a special step branches on the step's flags to one of six
+  scheduled blocks, one per path of its item (PATHS), each interleaving the
+  path's bias gather and softmax with the phase's products;
 * K tiles pass through one LDS slot per wavefront into two register
   buffers: in phase 0 of step j, after the score product of item (j, 1)
   read K(j), K(j + 2) is read from the slot into that buffer, and then
@@ -219,75 +222,107 @@ def gather_valu(J):
     return out
 
 
-def special_softmax(J, sl):
-    """Softmax of item (j, J) of a special step, after its bias gather, as
-    the general code forms it: y = s * scale + bias (masked keys -inf); at
-    the first step the running max from y (and the running sums scaled by
-    exp2(m_old - m_new)); then p = exp2(y - m) for band or masked items,
-    exp2(s * scale + (bias - m)) for plain ones.  Returns (text, path) where
-    path(needy, msk, first, gen) is the instruction sequence that runs."""
+# Special items by path: (needy, masked, first, general).  needy: y = s *
+# scale + bias is formed (the first step, band and masked items); masked: keys
+# >= LK get y = -inf; first: the running max is set from y (and the running
+# sums scaled by exp2(m_old - m_new)); general: p = exp2(y - m), else the plain
+# form exp2(s * scale + (bias - m)).  Masked items are general, and an item
+# is needy exactly when it is general or in the first step.
+PATHS = {"P": (0, 0, 0, 0), "G": (1, 0, 0, 1), "GM": (1, 1, 0, 1),
+         "F0": (1, 0, 1, 0), "FG": (1, 0, 1, 1), "FGM": (1, 1, 1, 1)}
+
+
+def auto_deps(seq):
+    """Orders a straight-line list for the list scheduler: each instruction
+    depends on every earlier one that writes a register it reads or writes,
+    or reads a register it writes."""
+    for i, c in enumerate(seq):
+        for p in seq[:i]:
+            if (p.writes & (c.reads | c.writes)) or (p.reads & c.writes):
+                if p.tag not in c.deps:
+                    c.deps.append(p.tag)
+    return seq
+
+
+def special_valu(J, path):
+    """Vector list of item (j, J) of a special step on one path: the bias
+    gather, then the softmax as the general code forms it (see PATHS),
+    straight-line, for the list scheduler to interleave with the phase's
+    products.  %[m J] (the running max) is tracked as the pseudo-register
+    mJ."""
+    needy, msk, first_step, general = PATHS[path]
     bf = J
     s = SACC[bf]
     m = f"%[m{J}]"
-    lab = {n: f"L_{n}{sl}{J}_%=" for n in ("noy", "nomask", "plain", "cvt")}
-    head = [Ins("s_waitcnt lgkmcnt(0)", "waitcnt"),
-            valu(f"v_mov_b32_e32 {x(1)}, {t(0)}", {t(0)}, {x(1)}),
-            salu(f"s_bitcmp1_b32 s{S_NEEDY}, {J}"), branch(f"s_cbranch_scc0 {lab['noy']}")]
-    ys = [valu(f"v_fma_f32 {t(i)}, v{s + i}, s{S_SCALE}, {t(i)}", {f"v{s + i}", t(i)}, {t(i)}) for i in range(16)]
-    chk_m = [salu(f"s_bitcmp1_b32 s{S_MSK}, {J}"), branch(f"s_cbranch_scc0 {lab['nomask']}")]
-    mask = [valu(f"v_sub_u32_e32 {x(0)}, s{S_LIM}, %[g8]", (), {x(0)}),
-            valu(f"v_mov_b32_e32 {x(3)}, 0xff800000", (), {x(3)})]
-    for i in range(16):
-        mask.append(valu(f"v_cmp_lt_i32_e32 vcc, {key_col(i)}, {x(0)}", {x(0)}, {"vcc"}))
-        mask.append(valu(f"v_cndmask_b32_e32 {t(i)}, {x(3)}, {t(i)}, vcc", {t(i), x(3), "vcc"}, {t(i)}))
-    chk_f = [salu(f"s_cmp_lg_u32 s{S_J}, 0"), branch(f"s_cbranch_scc1 {lab['noy']}")]
-    first = [valu(f"v_max3_f32 {x(0)}, {t(0)}, {t(1)}, {t(2)}", {t(0), t(1), t(2)}, {x(0)})]
-    for i in range(3, 15, 2):
-        first.append(valu(f"v_max3_f32 {x(0)}, {x(0)}, {t(i)}, {t(i + 1)}", {x(0), t(i), t(i + 1)}, {x(0)}))
-    first.append(valu(f"v_max_f32_e32 {x(0)}, {x(0)}, {t(15)}", {x(0), t(15)}, {x(0)}))
-    first += [valu(f"v_mov_b32_e32 {x(3)}, {x(0)}", {x(0)}, {x(3)}),
-              valu(f"v_mov_b32_e32 {x(4)}, {x(0)}", {x(0)}, {x(4)}),
-              Ins(f"v_permlane32_swap_b32_e32 {x(3)}, {x(4)}", "permlane", reads={x(3), x(4)}, writes={x(3), x(4)}),
-              valu(f"v_max3_f32 {x(0)}, {m}, {x(3)}, {x(4)}", {x(3), x(4)}, {x(0)}),
-              valu(f"v_sub_f32_e32 {x(2)}, {m}, {x(0)}", {x(0)}, {x(2)}),
-              valu(f"v_exp_f32_e32 {x(2)}, {x(2)}", {x(2)}, {x(2)}, kind="trans")]
-    first += [valu(f"v_mul_f32_e32 v{rs(J) + k}, v{rs(J) + k}, {x(2)}", {f"v{rs(J) + k}", x(2)}, {f"v{rs(J) + k}"})
-              for k in range(4)]
-    first.append(valu(f"v_mov_b32_e32 {m}, {x(0)}", {x(0)}, ()))
-    chk_g = [salu(f"s_bitcmp1_b32 s{S_GEN}, {J}"), branch(f"s_cbranch_scc0 {lab['plain']}")]
-    gen = []
-    for i in range(0, 16, 2):
-        gen += [valu(f"v_sub_f32_e32 {t(i)}, {t(i)}, {m}", {t(i)}, {t(i)}),
-                valu(f"v_sub_f32_e32 {t(i + 1)}, {t(i + 1)}, {m}", {t(i + 1)}, {t(i + 1)}),
-                valu(f"v_exp_f32_e32 {t(i)}, {t(i)}", {t(i)}, {t(i)}, kind="trans"),
-                valu(f"v_exp_f32_e32 {t(i + 1)}, {t(i + 1)}", {t(i + 1)}, {t(i + 1)}, kind="trans")]
-    gen.append(branch(f"s_branch {lab['cvt']}"))
-    plain = [valu(f"v_sub_f32_e32 {x(2)}, {x(1)}, {m}", {x(1)}, {x(2)})]
-    for i in range(0, 16, 2):
-        plain += [valu(f"v_fma_f32 {t(i)}, v{s + i}, s{S_SCALE}, {x(2)}", {f"v{s + i}", x(2)}, {t(i)}),
-                  valu(f"v_fma_f32 {t(i + 1)}, v{s + i + 1}, s{S_SCALE}, {x(2)}", {f"v{s + i + 1}", x(2)},
-                       {t(i + 1)}),
-                  valu(f"v_exp_f32_e32 {t(i)}, {t(i)}", {t(i)}, {t(i)}, kind="trans"),
-                  valu(f"v_exp_f32_e32 {t(i + 1)}, {t(i + 1)}", {t(i + 1)}, {t(i + 1)}, kind="trans")]
-    cvt = [nop(0)]
+    mr = f"m{J}"
+    tags = iter(range(1000))
+
+    def v(text, reads=(), writes=(), kind="valu"):
+        return valu(text, set(reads), set(writes), f"S{next(tags)}.{J}", kind)
+
+    gather = gather_valu(J)
+    ts = {t(i) for i in range(16)}
+    wait = Ins("s_waitcnt lgkmcnt(0)", "waitcnt", writes=ts, tag=f"W.{J}")   # the gathered biases have landed
+    seq = [wait] + ([] if general else [v(f"v_mov_b32_e32 {x(1)}, {t(0)}", {t(0)}, {x(1)})])
+    if needy:
+        seq += [v(f"v_fma_f32 {t(i)}, v{s + i}, s{S_SCALE}, {t(i)}", {f"v{s + i}", t(i)}, {t(i)}) for i in range(16)]
+    if msk:
+        seq += [v(f"v_sub_u32_e32 {x(0)}, s{S_LIM}, %[g8]", (), {x(0)}),
+                v(f"v_mov_b32_e32 {x(3)}, 0xff800000", (), {x(3)})]
+        for i in range(16):
+            seq.append(v(f"v_cmp_lt_i32_e32 vcc, {key_col(i)}, {x(0)}", {x(0)}, {"vcc"}))
+            seq.append(v(f"v_cndmask_b32_e32 {t(i)}, {x(3)}, {t(i)}, vcc", {t(i), x(3), "vcc"}, {t(i)}))
+    if first_step:
+        seq.append(v(f"v_max3_f32 {x(0)}, {t(0)}, {t(1)}, {t(2)}", {t(0), t(1), t(2)}, {x(0)}))
+        for i in range(3, 15, 2):
+            seq.append(v(f"v_max3_f32 {x(0)}, {x(0)}, {t(i)}, {t(i + 1)}", {x(0), t(i), t(i + 1)}, {x(0)}))
+        seq += [v(f"v_max_f32_e32 {x(0)}, {x(0)}, {t(15)}", {x(0), t(15)}, {x(0)}),
+                v(f"v_mov_b32_e32 {x(3)}, {x(0)}", {x(0)}, {x(3)}),
+                v(f"v_mov_b32_e32 {x(4)}, {x(0)}", {x(0)}, {x(4)}),
+                v(f"v_permlane32_swap_b32_e32 {x(3)}, {x(4)}", {x(3), x(4)}, {x(3), x(4)}, "permlane"),
+                v(f"v_max3_f32 {x(0)}, {m}, {x(3)}, {x(4)}", {x(3), x(4), mr}, {x(0)}),
+                v(f"v_sub_f32_e32 {x(2)}, {m}, {x(0)}", {x(0), mr}, {x(2)}),
+                v(f"v_exp_f32_e32 {x(2)}, {x(2)}", {x(2)}, {x(2)}, "trans")]
+        seq += [v(f"v_mul_f32_e32 v{rs(J) + k}, v{rs(J) + k}, {x(2)}", {f"v{rs(J) + k}", x(2)}, {f"v{rs(J) + k}"})
+                for k in range(4)]
+        seq.append(v(f"v_mov_b32_e32 {m}, {x(0)}", {x(0)}, {mr}))
+    if general:
+        for i in range(16):
+            seq.append(v(f"v_sub_f32_e32 {t(i)}, {t(i)}, {m}", {t(i), mr}, {t(i)}))
+            seq.append(v(f"v_exp_f32_e32 {t(i)}, {t(i)}", {t(i)}, {t(i)}, "trans"))
+    else:
+        seq.append(v(f"v_sub_f32_e32 {x(2)}, {x(1)}, {m}", {x(1), mr}, {x(2)}))
+        for i in range(16):
+            seq.append(v(f"v_fma_f32 {t(i)}, v{s + i}, s{S_SCALE}, {x(2)}", {f"v{s + i}", x(2), t(i)}, {t(i)}))
+            seq.append(v(f"v_exp_f32_e32 {t(i)}, {t(i)}", {t(i)}, {t(i)}, "trans"))
     for k in range(8):
         hh, r = k >> 2, k & 3
-        cvt.append(valu(f"v_cvt_pk_f16_f32 v{pk(bf, hh) + r}, {t(2 * k)}, {t(2 * k + 1)}", {t(2 * k), t(2 * k + 1)},
-                        {f"v{pk(bf, hh) + r}"}))
-    cvt.append(nop(1))
-    for seq in (first, gen, plain, mask):
-        G.pad(seq)
-    text = (head + ys + chk_m + mask + [label(lab["nomask"])] + chk_f + first + [label(lab["noy"])] + chk_g + gen
-            + [label(lab["plain"])] + plain + [label(lab["cvt"])] + cvt)
+        c = v(f"v_cvt_pk_f16_f32 v{pk(bf, hh) + r}, {t(2 * k)}, {t(2 * k + 1)}", {t(2 * k), t(2 * k + 1)},
+              {f"v{pk(bf, hh) + r}"})
+        c.deps += [f"P{hh}0.{J}", f"P{hh}1.{J}"]   # after the PV products that read the previous contents
+        seq.append(c)
+    out = gather + seq
+    auto_deps(out)
+    return out
 
-    def path(needy, msk, first_step, general):
-        seq = list(head)
-        if needy:
-            seq += ys + chk_m + (mask if msk else []) + [label(lab["nomask"])] + chk_f + (first if first_step else [])
-        seq += [label(lab["noy"])] + chk_g
-        seq += (gen if general else [label(lab["plain"])] + plain) + [label(lab["cvt"])] + cvt
-        return seq
-    return text, path
+
+def dispatch(sl, J):
+    """SALU branches from the step's flags to the scheduled variant of the
+    item's path (wave-uniform), as (text, {path: executed prefix})."""
+    lab = {pth: f"L_v{sl}{J}{pth}_%=" for pth in PATHS}
+    lf = f"L_vf{sl}{J}_%="
+    c_needy = [salu(f"s_bitcmp1_b32 s{S_NEEDY}, {J}"), branch(f"s_cbranch_scc0 {lab['P']}")]
+    c_first = [salu(f"s_cmp_eq_u32 s{S_J}, 0"), branch(f"s_cbranch_scc1 {lf}")]
+    c_msk = [salu(f"s_bitcmp1_b32 s{S_MSK}, {J}"), branch(f"s_cbranch_scc1 {lab['GM']}"),
+             branch(f"s_branch {lab['G']}")]
+    c_gen = [label(lf), salu(f"s_bitcmp1_b32 s{S_GEN}, {J}"), branch(f"s_cbranch_scc0 {lab['F0']}")]
+    c_fmsk = [salu(f"s_bitcmp1_b32 s{S_MSK}, {J}"), branch(f"s_cbranch_scc1 {lab['FGM']}"),
+              branch(f"s_branch {lab['FG']}")]
+    text = c_needy + c_first + c_msk + c_gen + c_fmsk
+    executed = {"P": c_needy, "G": c_needy + c_first + c_msk, "GM": c_needy + c_first + c_msk[:2],
+                "F0": c_needy + c_first + c_gen, "FG": c_needy + c_first + c_gen + c_fmsk,
+                "FGM": c_needy + c_first + c_gen + c_fmsk[:2]}
+    return text, {pth: seq + [label(lab[pth])] for pth, seq in executed.items()}, lab
 
 
 def plain_step(sl, history):
@@ -301,14 +336,36 @@ def plain_step(sl, history):
 
 
 def special_step(sl, history):
+    """Both phases of a special step: for each, the dispatch to one scheduled
+    block per path (the phase's products interleaved with the gather and the
+    path's softmax), each ending at the phase's join.  Returns (text, phases)
+    with phases[J] = {path: executed sequence of phase J on that path}."""
     text, phases = [], []
     for J in range(NBLK):
-        mf, pre, post = skeleton(J, sl, special=True)
-        part_a, _ = schedule(mf, pre, post, gather_valu(J), history)
-        sm_text, sm_path = special_softmax(J, sl)
-        text += part_a + sm_text
-        phases.append((part_a, sm_path))
-        history = part_a + sm_path(1, 1, 1, 1)
+        d_text, d_exec, lab = dispatch(sl, J)
+        join = f"L_vj{sl}{J}_%="
+        text += d_text
+        variants = {}
+        for pth in PATHS:
+            mf, pre, post = skeleton(J, sl, special=True)
+            # the phase's memory operations keep their place before any
+            # vector instruction that touches their registers (the K copy
+            # offsets in v145-v148 are softmax temporaries)
+            ops = [o for mm in mf for o in pre[mm.tag] + post[mm.tag]]
+            for i, o in enumerate(ops):
+                o.tag = o.tag or f"X{i}.{J}"
+            vl = special_valu(J, pth)
+            for c in vl:
+                for o in ops:
+                    if (c.writes & (o.reads | o.writes)) or (c.reads & o.writes):
+                        c.deps.append(o.tag)
+            block, _ = schedule(mf, pre, post, vl, history)
+            block.append(nop(1))   # its last vector writes -> the next phase's first products
+            text += [label(lab[pth])] + block + [branch(f"s_branch {join}")]
+            variants[pth] = d_exec[pth] + block + [branch(f"s_branch {join}"), label(join)]
+        text.append(label(join))
+        phases.append(variants)
+        history = variants["FGM"]
     return text, phases
 
 
@@ -493,33 +550,31 @@ def build():
     for seq in (FENCE + e0 + e1 + e0 + tail + FENCE, FENCE + e1 + e0 + e1 + tail + FENCE,
                 FENCE + e0 + tail + FENCE, FENCE + e1 + tail + FENCE, FENCE + pe + e0 + tail, FENCE + pe + e1 + tail):
         check_hazards(seq)
-    paths = [p for p in itertools.product((0, 1), repeat=4) if p[0] == (p[3] or p[2]) and not (p[1] and not p[3])]
     for sl in (0, 1):
         phases = sp_phases[sl]
         for J in range(NBLK):
-            a_j, path_j = phases[J]
             if J == 0:
-                a3, path3 = sp_phases[sl ^ 1][NBLK - 1]
-                befores = [FENCE + pre] + [a3 + path3(*p) + [salu("s_add_u32"), branch("s_branch")] + pre
-                                           for p in paths]
+                befores = [FENCE + pre] + [v + [salu("s_add_u32"), branch("s_branch")] + pre
+                                           for v in sp_phases[sl ^ 1][NBLK - 1].values()]
             else:
-                befores = [phases[J - 1][0] + phases[J - 1][1](*p) for p in paths]
-            afters = ([phases[J + 1][0][:40]] if J < NBLK - 1 else
-                      [pre + sp_phases[sl ^ 1][0][0][:40], pe + s0[:40], pe + s1[:40], tail + FENCE])
+                befores = list(phases[J - 1].values())
+            afters = (list(phases[J + 1].values()) if J < NBLK - 1 else
+                      [pre + v for v in sp_phases[sl ^ 1][0].values()] + [pe + s0[:40], pe + s1[:40], tail + FENCE])
             for before in befores:
-                for p in paths:
+                for seq in phases[J].values():
                     for after in afters:
-                        check_hazards(before[-40:] + a_j + path_j(*p) + after)
+                        check_hazards(before[-40:] + seq + after[:60])
     # outstanding loads: entry state K(1) loads done, V(0) landed in slot 0
+    # (each phase of two special steps on every path, the others on FGM)
     for first in (0, 1):
-        seq = []
-        for sl in (first, first ^ 1):
-            for J in range(NBLK):
-                a_j, path_j = sp_phases[sl][J]
-                seq += a_j + path_j(1, 1, 1, 1)
-        seq += pe + (s0 + s1 + s0 if first == 0 else s1 + s0 + s1)
-        vm = check_waits(seq, [])
-        assert len(vm) <= 8, vm
+        slots = [(sl, J) for sl in (first, first ^ 1) for J in range(NBLK)]
+        for at, pth in itertools.product(range(len(slots)), PATHS):
+            seq = []
+            for k, (sl, J) in enumerate(slots):
+                seq += sp_phases[sl][J][pth if k == at else "FGM"]
+            seq += pe + (s0 + s1 + s0 if first == 0 else s1 + s0 + s1)
+            vm = check_waits(seq, [])
+            assert len(vm) <= 8, vm
     # every exit (after the special steps, after an even or an odd plain
     # step) leaves nothing in flight
     for seq in (pe + tail, pe + s0 + advance() + tail, pe + s1 + advance() + tail,
