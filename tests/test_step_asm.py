@@ -3,6 +3,9 @@
 * The generator's checks (csrc/gen_w64_step.py over csrc/gen_asm.py) pass
   on the loop it writes, and they catch planted mistakes: a removed wait
   state, a missing LDS wait, a missing copy wait, a missing wait at the exit.
+* The special steps' per-path blocks: the softmax shares its block with the
+  phase's products, and no copy's offset register is overwritten before
+  the copy reads it.
 * Operand placement in the compiled kernel: the loop's text names fixed
   registers (v0-v148, v152-v231, s64-s95);
   every register the compiler substituted for a named operand must lie
@@ -180,3 +183,61 @@ def test_compiled_operands_avoid_the_loop_registers(kernel):
     # every input the loop reads is bound
     for name in inputs:
         assert name in bound, name
+
+
+def _special_blocks(gen):
+    """{(slot parity, phase, path): scheduled block} of the special steps."""
+    pre = gen.special_preamble()
+    out = {}
+    for sl in (0, 1):
+        _, phases = gen.special_step(sl, gen.FENCE + pre)
+        for J, variants in enumerate(phases):
+            for pth, seq in variants.items():
+                start = max(k for k, ins in enumerate(seq) if ins.kind == "label" and f"L_v{sl}{J}{pth}_" in ins.text)
+                out[(sl, J, pth)] = seq[start + 1:]
+    return out
+
+
+def test_special_step_paths_interleave_their_softmax_with_the_products():
+    """Each phase of a special step has one scheduled block per path of its
+    item; the softmax (after the gathered biases' wait) shares its block with
+    the phase's products rather than following all of them, and the six
+    paths cover the general code's cases."""
+    gen = _gen()
+    assert set(gen.PATHS) == {"P", "G", "GM", "F0", "FG", "FGM"}
+    for (sl, J, pth), block in _special_blocks(gen).items():
+        kinds = [ins.kind for ins in block]
+        assert kinds.count("mfma") == 10, (sl, J, pth)
+        wait = next(k for k, ins in enumerate(block) if ins.tag == f"W.{J}")   # the gathered biases
+        softmax = next(k for k in range(wait + 1, len(block)) if block[k].kind in ("valu", "trans"))
+        last_mfma = max(k for k, kind in enumerate(kinds) if kind == "mfma")
+        assert softmax < last_mfma, (sl, J, pth)
+        exps = sum(1 for ins in block if ins.text.startswith("v_exp_f32"))
+        assert exps == 16 + (1 if pth.startswith("F") else 0), (sl, J, pth)
+
+
+def test_special_step_copies_read_their_offsets_before_the_softmax_reuses_them():
+    """The K copies of a special step take their lane offsets from v145-v148,
+    which the softmax also uses as temporaries: in every scheduled block no
+    instruction writes a copy's offset register before that copy, and the
+    check this test applies catches a planted write."""
+    gen = _gen()
+
+    def check(block):
+        for k, ins in enumerate(block):
+            if ins.kind != "dma":
+                continue
+            for prev in block[:k]:
+                assert not (prev.writes & ins.reads - {"m0"}), (prev.text, ins.text)
+
+    blocks = _special_blocks(gen)
+    for block in blocks.values():
+        check(block)
+    block = next(b for (sl, J, pth), b in blocks.items() if J == 0 and pth == "FG")
+    dmas = [k for k, ins in enumerate(block) if ins.kind == "dma" and ins.reads & {"v145", "v146", "v147", "v148"}]
+    assert len(dmas) == 4
+    dma = dmas[0]
+    writer = next(ins for ins in block[dma:] if ins.writes & block[dmas[-1]].reads - {"m0"})  # e.g. the max's temporaries
+    planted = block[:dma] + [writer] + block[dma:]
+    with pytest.raises(AssertionError):
+        check(planted)
