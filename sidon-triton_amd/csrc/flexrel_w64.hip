@@ -10,7 +10,7 @@
 // 4 wavefronts; wavefront w runs an online softmax for all 64 rows (two
 // 32-query column blocks) over the key steps w, w + 4, w + 8, ... (32 keys
 // each), and the four partial results are merged through LDS at the end.
-// A workgroup needs at most 256 registers per lane and 71 KB of LDS, so two
+// A workgroup needs at most 256 registers per lane and 73 KB of LDS, so two
 // workgroups share a compute unit: every SIMD runs two wavefronts, and one
 // issues its vector work while the other's products hold the matrix core
 // (one wavefront alone issues a vector instruction only every ~5.4 cycles,
