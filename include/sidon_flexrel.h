@@ -105,6 +105,18 @@ int sidon_flexrel_launch_shape(int B, int H, int L, int* queries_per_block,
                                int* key_splits, int* workgroups,
                                int* threads_per_block);
 
+/*
+ * Test hook.  With `on` nonzero, every wavefront of the 64-row kernel
+ * discards what its hand-scheduled key-step loop computed and runs its steps
+ * again through the kernel's compiled general code -- the path a wavefront
+ * takes when a probability leaves the fp16 range -- so that tests can require
+ * the two to agree bit for bit on every row.  Process-wide; read by every
+ * sidon_flexrel_fwd / sidon_flexrel_fwd_qkv call (a captured graph keeps the
+ * value of its capture).  Slower; never needed in production.  Has no
+ * counterpart in the reference.
+ */
+void sidon_flexrel_debug_rerun_all(int on);
+
 /* Thread-local text of the last error ("" when none). */
 const char* sidon_last_error(void);
 

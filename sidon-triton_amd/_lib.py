@@ -34,6 +34,7 @@ SIGNATURES = {
                                              ctypes.c_int, _VP]),
     "sidon_flexrel_launch_shape": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int, _IP, _IP,
                                                   _IP, _IP]),
+    "sidon_flexrel_debug_rerun_all": (None, [ctypes.c_int]),
     "sidon_res_norm": (ctypes.c_int, [_VP, _VP, _VP, _VP, _VP, ctypes.c_float, ctypes.c_int, _VP, _VP,
                                       ctypes.c_float, _VP, ctypes.c_int, ctypes.c_int, ctypes.c_int, _VP]),
     "sidon_glu": (ctypes.c_int, [_VP, _VP, ctypes.c_int, ctypes.c_int, _VP]),

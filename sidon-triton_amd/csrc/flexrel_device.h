@@ -49,6 +49,7 @@ struct Params {
   int nqb;                 // query blocks per (b, h) in this launch
   int row0;                // first query row of block 0 (a launch may cover rows [row0, L))
   float scale;             // log2(e) / sqrt(64)
+  int rerun_all;           // test hook (sidon_flexrel_debug_rerun_all): every 64-row wavefront reruns
 };
 
 // 16-byte chunk c of tile row r is stored at chunk position c ^ tile_swz(r)

@@ -58,6 +58,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <atomic>
 #include <mutex>
 #include <type_traits>
 
@@ -750,6 +751,8 @@ namespace {
 // (flexrel_w32.hip) for short sequences.
 enum Variant { kSplit8 = 0, kW64 = 3, kW32 = 4 };
 
+std::atomic<int> g_rerun_all{0};  // sidon_flexrel_debug_rerun_all
+
 // SIDON_FLEXREL_VARIANT=split8|w64|w32 forces one variant (A/B timing and
 // tests); unset, empty or "auto" picks by shape; any other value is an error
 // (SIDON_E_CONFIG), so a mistyped override never runs silently on the
@@ -908,6 +911,7 @@ SIDON_API int sidon_flexrel_fwd(const void* q, const void* k, const void* v, con
   p.H = H;
   p.L = L;
   p.scale = 1.4426950408889634f / 8.0f;  // log2(e) / sqrt(64)
+  p.rerun_all = g_rerun_all.load(std::memory_order_relaxed);
 
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   hipError_t err = hipSuccess;
@@ -943,6 +947,14 @@ SIDON_API int sidon_flexrel_fwd_qkv(const void* qkv, const void* rel, const int3
   return sidon_flexrel_fwd(base, base + hid, base + 2 * hid, rel, lens, out, B, H, L, kD, in_st,
                            in_st, in_st, out_st, stream);
 }
+
+// Test hook: with `on` nonzero, every wavefront of the 64-row kernel discards
+// its hand-scheduled loop's results and runs its steps again through the
+// compiled general code (the path a wavefront takes when a probability
+// leaves the fp16 range), so that the two can be compared bit for bit on
+// every row.  Read at each sidon_flexrel_fwd call (a captured graph keeps the
+// value of its capture).
+SIDON_API void sidon_flexrel_debug_rerun_all(int on) { g_rerun_all.store(on != 0, std::memory_order_relaxed); }
 
 SIDON_API const char* sidon_last_error(void) { return sidon::g_err; }
 

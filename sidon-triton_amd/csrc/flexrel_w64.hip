@@ -588,7 +588,7 @@ flexrel_w64_kernel(const Params p) {
       // register outputs -- the V^T operands read below among them -- are
       // final: a wait placed here in compiled code would not order the
       // register-only products after it.)
-      if (__builtin_expect(overflow != 0, 0)) continue;
+      if (__builtin_expect(overflow != 0 || p.rerun_all != 0, 0)) continue;
       pv(0, 0);  // PV of items (nu - 1, 0) and (nu - 1, 1)
       pv(1, 1);
       break;

@@ -153,3 +153,70 @@ def test_different_kv_strides_take_the_8_split_kernel(sidon, monkeypatch):
     monkeypatch.setenv("SIDON_FLEXREL_VARIANT", "split8")
     out8 = run(sidon, q, k, v, rel)
     assert torch.equal(out, out8)
+
+
+RERUN_SHAPES = [
+    # (B, H, L, lens): plain, band, straddling and first-step paths; one 64-row
+    # workgroup per CU and two; wavefronts with no step (L < 4 x 32)
+    (1, 2, 33, [20]),
+    (2, 2, 200, [200, 173]),
+    (3, 2, 300, [300, 64, 129]),
+    (2, 16, 600, [600, 517]),
+    (1, 16, 1500, [1463]),
+    (1, 16, 2990, None),
+    (1, 16, 4800, None),
+]
+
+
+@pytest.mark.parametrize("B,H,L,lens", RERUN_SHAPES)
+def test_w64_loop_matches_its_general_code_bit_for_bit(sidon, monkeypatch, B, H, L, lens):
+    """The 64-row kernel's hand-scheduled key-step loop -- its plain steps and
+    the scheduled block of every special-step path -- against the kernel's
+    compiled general code, which a wavefront reruns when a probability leaves
+    the fp16 range: with every wavefront forced onto that rerun
+    (sidon_flexrel_debug_rerun_all), every output element, padded rows
+    included, is bit-identical to the loop's."""
+    monkeypatch.setenv("SIDON_FLEXREL_VARIANT", "w64")
+    q, k, v, rel = seeded_inputs(B, H, L, seed=3000 + L)
+    lib = sidon._lib.load()
+    loop = run(sidon, q, k, v, rel, lens).cpu()
+    lib.sidon_flexrel_debug_rerun_all(1)
+    try:
+        general = run(sidon, q, k, v, rel, lens).cpu()
+    finally:
+        lib.sidon_flexrel_debug_rerun_all(0)
+    assert torch.equal(loop, general), int((loop != general).sum())
+
+
+def test_rerun_hook_takes_the_general_code(sidon, monkeypatch):
+    """The hook is live: with every wavefront on the compiled general code the
+    c3 layer takes several times as long as the hand-scheduled loop (so the
+    bit-identity above compares two different code paths)."""
+    monkeypatch.setenv("SIDON_FLEXREL_VARIANT", "w64")
+    L, H = 4800, 16
+    gen = torch.Generator().manual_seed(L)
+    qkv = torch.randn(L, 3 * H * 64, generator=gen).half().to(DEV)
+    rel = (torch.randn(73, 64, generator=gen) * 0.02).half().to(DEV)
+    lens = torch.tensor([L], dtype=torch.int32, device=DEV)
+    out = torch.empty(L, H * 64, dtype=torch.float16, device=DEV)
+    lib = sidon._lib.load()
+
+    def ms():
+        for _ in range(3):
+            sidon.encoder_attention.flexrel_attention(qkv, 1, H, rel, lens, out=out)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(10):
+            sidon.encoder_attention.flexrel_attention(qkv, 1, H, rel, lens, out=out)
+        e1.record()
+        e1.synchronize()
+        return e0.elapsed_time(e1) / 10
+
+    fast = ms()
+    lib.sidon_flexrel_debug_rerun_all(1)
+    try:
+        slow = ms()
+    finally:
+        lib.sidon_flexrel_debug_rerun_all(0)
+    print(f"c3 layer: loop {fast:.3f} ms, every wavefront rerun {slow:.3f} ms", flush=True)
+    assert slow > 1.5 * fast
